@@ -1,0 +1,171 @@
+#!/usr/bin/env python3
+"""Benchmark of the alignment hot path on one MI355X.
+
+Workload: config C2 (B=64 wav2vec2-char-shaped records, T~U{250..1750}, V=32,
+peaky synthetic emissions), optimized mode, inputs resident in HBM. A step is
+one ``align`` call over the whole batch (host preparation, descriptor upload,
+kernels); K steps run back to back with no host synchronization in between.
+
+Prints one JSON line: aligned frames/s as ``value``, DP cells/s, the dominant
+kernel's HBM roofline fraction (kernel duration from HIP events recorded on the
+launch stream around that kernel in every timed step), the same figures for
+conventional mode, and a CPU baseline (the oracle's conventional DP on the
+host cores, a bounded sample of the same batch).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for path in (REPO, REPO / "fast-forced-aligner_amd"):
+    if str(path) not in sys.path:
+        sys.path.insert(0, str(path))
+
+METRIC = "aligned frames/sec + DP cells/sec on 1 MI355X; % of HBM roofline"
+HBM_PEAK_GBS = 8000.0
+
+
+def hip_runtime():
+    lib = ctypes.CDLL("libamdhip64.so.7")
+    lib.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+    lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+    return lib
+
+
+def measure(ffa, capi_lib, hip, es, ys, mode, steps, warmup):
+    import torch
+
+    for _ in range(warmup):
+        ffa.align(es, ys, mode=mode)
+    torch.cuda.synchronize()
+    starts, stops = [], []
+    for _ in range(steps):
+        a, b = ctypes.c_void_p(), ctypes.c_void_p()
+        assert hip.hipEventCreate(ctypes.byref(a)) == 0 and hip.hipEventCreate(ctypes.byref(b)) == 0
+        starts.append(a)
+        stops.append(b)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        capi_lib.ffa_profile_next_launch(starts[i], stops[i])
+        result = ffa.align(es, ys, mode=mode)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    kernel_ms = []
+    for a, b in zip(starts, stops):
+        ms = ctypes.c_float()
+        assert hip.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+        kernel_ms.append(ms.value)
+        hip.hipEventDestroy(a)
+        hip.hipEventDestroy(b)
+    return elapsed / steps, sum(kernel_ms) / len(kernel_ms), result
+
+
+def cpu_baseline(batch, seconds=10.0):
+    """The oracle's conventional DP (same recurrence and tie rule as the
+    reference's conventional mode) on host threads, one record per task."""
+    from oracle import oracle
+
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    cores = max(1, min(cores, 16))
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.align(batch.emissions, batch.targets, mode="conventional", threads=cores)
+        reps += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    elapsed = time.perf_counter() - t0
+    return {"value": batch.frames * reps / elapsed, "unit": "aligned frames/s", "cores": cores, "kind": "port",
+            "dp_cells_per_s": batch.cells * reps / elapsed,
+            "sample": f"{batch.name} full batch x{reps} ({elapsed:.1f} s), conventional DP, C oracle, "
+                      f"one record per thread"}
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    parser.add_argument("--mode", default="optimized", choices=["optimized", "conventional"])
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    parser.add_argument("--no-conventional", action="store_true", help="skip the conventional-mode figures")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: the alignment path has no multi-GPU mode in this build "
+              f"(records are independent; see DESIGN.md for how a batch would shard). Got --gpus {args.gpus}.",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import fast_forced_aligner as ffa
+    from fast_forced_aligner import capi, workloads
+
+    batch = workloads.make(args.config)
+    dev = "cuda:0"
+    es = [torch.from_numpy(e).to(dev) for e in batch.emissions]
+    ys = [torch.from_numpy(y).to(dev) for y in batch.targets]
+    ffa.load_extension()
+    capi_lib = capi.load()
+    hip = hip_runtime()
+    min_bytes = batch.min_bytes()
+
+    def figures(mode, steps, warmup):
+        step_s, kernel_ms, result = measure(ffa, capi_lib, hip, es, ys, mode, steps, warmup)
+        achieved = min_bytes / (kernel_ms * 1e-3) / 1e9
+        return step_s, kernel_ms, achieved, result
+
+    step_s, kernel_ms, achieved, result = figures(args.mode, args.steps, args.warmup)
+    # parity spot check outside the timed region
+    from oracle import oracle
+    want = oracle.align(batch.emissions, batch.targets, mode=args.mode, threads=8)
+    parity = bool(np.array_equal(result.labels.cpu().numpy(), want["labels"]) and
+                  np.array_equal(result.scores.cpu().numpy().view(np.int32), want["scores"].view(np.int32)) and
+                  np.array_equal(result.status.cpu().numpy(), want["status"]))
+    line = {
+        "metric": METRIC,
+        "value": batch.frames / step_s,
+        "unit": "aligned frames/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": step_s * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"{args.config}: {len(es)} records, {batch.frames} frames, V="
+                               f"{batch.emissions[0].shape[1]}, {args.mode} mode",
+                   "mode": args.mode, "records": len(es), "frames": batch.frames, "dp_cells": batch.cells},
+        "dp_cells_per_s": batch.cells / step_s,
+        "parity_vs_oracle": parity,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "chunk_kernel" if args.mode == "optimized" else "conventional_kernel",
+                     "kernel_us": kernel_ms * 1e3, "algorithmic_bytes": min_bytes},
+    }
+    if not args.no_conventional and args.mode == "optimized":
+        c_step, c_kernel_ms, c_achieved, _ = figures("conventional", max(10, args.steps // 10), 3)
+        line["conventional"] = {"ms_per_step": c_step * 1e3, "frames_per_s": batch.frames / c_step,
+                                "dp_cells_per_s": batch.cells / c_step, "kernel_us": c_kernel_ms * 1e3,
+                                "roofline_frac": c_achieved / HBM_PEAK_GBS}
+    line["cpu_baseline"] = None if args.no_cpu else cpu_baseline(batch)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

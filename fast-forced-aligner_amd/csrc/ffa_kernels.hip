@@ -1,0 +1,1305 @@
+// CTC forced-alignment kernels for MI355X (gfx950) and the C ABI of include/ffa.h.
+//
+// One HIP source, no other backend. Reference behaviour is cited as
+// "cu:<line>" (src/fast_forced_aligner/csrc/alignment.cu) and "py:<line>"
+// (src/fast_forced_aligner/alignment.py).
+//
+// Work decomposition
+//   conventional mode: one launch, one workgroup per record. The workgroup
+//     validates the targets, runs the Viterbi recurrence over all T frames with
+//     2-bit backpointers in HBM, picks the terminal, walks the path back and
+//     writes labels and scores (cu:919-1061 sequence pack -> recurrence -> finish).
+//   optimized mode: two launches.
+//     pack_kernel: one workgroup per record: statuses, diagnostics, chunk slots.
+//     chunk_kernel: one workgroup per 128-frame chunk: greedy shortcut
+//       (cu:30-153) or relaxed chunk DP (cu:355-523) writes the chunk's labels
+//       and scores directly; the last chunk of a record to finish (atomic
+//       arrival counter) runs the record tail: repair planning (cu:164-228),
+//       repair DP, seam validation (cu:562-592), full-DP fallback and its path.
+//
+// DP layout: a workgroup of NT = 64*W threads owns the 2L+1 states of one
+// record, K contiguous states per thread (state s = tid*K + k). The s-1 / s-2
+// neighbours of a thread's first two states come from the previous lane via
+// DPP wave_shr:1, and across waves through a double-buffered LDS slot with one
+// barrier per frame. Emission gathers e[t][l[s]] are issued D frames ahead into
+// registers. Backpointers are 2 bits per state, 16 states per 32-bit word,
+// rows of 2*ceil(S/32) words.
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "ffa.h"
+
+namespace ffa {
+
+constexpr float NEG_INF = -INFINITY;
+constexpr int MAX_H = 512;          // chunk_frames supported by the LDS layout
+constexpr int TAIL_SLOT_CAP = 512;  // record tails with more chunks plan in global memory
+
+struct RecordDesc {  // device descriptor table entry, 64 bytes
+  const float* emissions;
+  const int64_t* targets;
+  int64_t frames;
+  int64_t frame_offset;     // into labels / scores
+  int64_t bp_offset;        // 32-bit words into the backpointer scratch
+  int64_t frontier_offset;  // floats into the frontier scratch; -1 when unused
+  int32_t vocab, tokens, blank, chunk_offset;
+};
+static_assert(sizeof(RecordDesc) == 64, "descriptor layout");
+
+struct Slot {  // per-chunk state of optimized mode (cu:1021-1029 buffers), 32 bytes
+  int32_t a, b, flag, start, end, shortcut, frontier_end;
+  float objective;
+};
+static_assert(sizeof(Slot) == 32, "slot layout");
+
+struct Params {
+  const RecordDesc* desc;
+  const int32_t* slot_record;
+  const uint8_t* validity;
+  int64_t* labels;
+  float* scores;
+  int32_t* status;
+  float* objective;
+  int32_t* stitched;
+  int32_t* repair_passes;
+  int64_t* repaired_frames;
+  int64_t* shortcut_stats;
+  int32_t* routing_stats;
+  int64_t* reuse_stats;
+  uint32_t* bp;
+  Slot* slots;
+  int32_t* arrivals;
+  float* frontiers;
+  int64_t budget, repair_min, frontier_min;
+  int32_t count, total_slots, H, mode, repair_rounds, check_inputs, overlap, frontier_batch;
+  int32_t u_cap, d_cap, v_words, lds_greedy, lds_tail_slots;
+};
+
+// ---------------------------------------------------------------------------
+// Shared-memory layout. A fixed header followed by dynamic regions whose sizes
+// come from the launch (all offsets are uniform).
+struct Header {
+  float xchg[2][16][2];  // DP neighbour values crossing wave boundaries
+  float red_v[16];
+  int red_i[16];
+  float term_v[2];
+  int ibuf[8];
+  float fbuf[4];
+};
+
+struct Lds {
+  Header* h;
+  int16_t* ytok;  // targets as int16 (V <= 8192)
+  // greedy region (aliased by the tail's slot copy)
+  int32_t* g;
+  float* fs;
+  int32_t* r;
+  int32_t* pd;
+  int32_t* pc;
+  int16_t* sym;
+  uint32_t* bitmap;
+  uint32_t* wpref;
+  Slot* tslots;
+};
+
+__device__ inline size_t align16(size_t x) { return (x + 15) & ~size_t(15); }
+
+__device__ inline Lds carve(unsigned char* base, const Params& p) {
+  Lds L;
+  size_t off = 0;
+  L.h = reinterpret_cast<Header*>(base);
+  off = align16(sizeof(Header));
+  L.ytok = reinterpret_cast<int16_t*>(base + off);
+  off = align16(off + 2 * (size_t)p.u_cap);
+  unsigned char* region = base + off;
+  size_t g = 0;
+  L.g = reinterpret_cast<int32_t*>(region + g); g += 4 * (size_t)p.H;
+  L.fs = reinterpret_cast<float*>(region + g); g += 4 * (size_t)p.H;
+  L.r = reinterpret_cast<int32_t*>(region + g); g += 4 * (size_t)p.H;
+  L.pd = reinterpret_cast<int32_t*>(region + g); g += 4 * (size_t)p.H;
+  L.pc = reinterpret_cast<int32_t*>(region + g); g += 4 * (size_t)p.H;
+  L.sym = reinterpret_cast<int16_t*>(region + g); g = align16(g + 2 * (size_t)p.d_cap);
+  L.bitmap = reinterpret_cast<uint32_t*>(region + g); g += 4 * (size_t)p.v_words;
+  L.wpref = reinterpret_cast<uint32_t*>(region + g);
+  L.tslots = reinterpret_cast<Slot*>(region);
+  return L;
+}
+
+// Loads through the global address space: the pointers come from the
+// descriptor table, so the compiler cannot infer it and would emit flat loads.
+typedef const __attribute__((address_space(1))) char gchar_t;
+__device__ inline float ldg_at(const void* base, uint32_t byte_offset) {
+  return *(const __attribute__((address_space(1))) float*)((gchar_t*)base + byte_offset);
+}
+
+// ---------------------------------------------------------------------------
+// Wave64 helpers.
+__device__ inline float wave_shr1(float x, float fill) {
+  // DPP wave_shr:1 - lane i receives lane i-1; lane 0 keeps `fill`.
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+      __builtin_bit_cast(int, fill), __builtin_bit_cast(int, x), 0x138, 0xf, 0xf, false));
+}
+
+// argmax with the reference's comparator (value desc, state asc; NaN never wins),
+// cu:472-491.
+__device__ inline void better(float& bv, int& bi, float ov, int oi) {
+  if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+}
+
+__device__ inline void wave_argmax(float& bv, int& bi) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, 64);
+    const int oi = __shfl_xor(bi, off, 64);
+    better(bv, bi, ov, oi);
+  }
+}
+
+__device__ inline int wave_incl_scan(int x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  return x;
+}
+
+// Block-wide inclusive scan of one int per thread (values beyond n are 0).
+__device__ inline int block_incl_scan(int x, Header* h) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  int v = wave_incl_scan(x);
+  __syncthreads();
+  if (lane == 63) h->red_i[wave] = v;
+  __syncthreads();
+  int carry = 0;
+  for (int w = 0; w < wave; ++w) carry += h->red_i[w];
+  (void)nw;
+  __syncthreads();
+  return v + carry;
+}
+
+__device__ inline int block_sum(int x, Header* h) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+  __syncthreads();
+  if (lane == 0) h->red_i[wave] = x;
+  __syncthreads();
+  int total = 0;
+  for (int w = 0; w < nw; ++w) total += h->red_i[w];
+  __syncthreads();
+  return total;
+}
+
+__device__ inline int block_min(int x, Header* h) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x = min(x, __shfl_xor(x, off, 64));
+  __syncthreads();
+  if (lane == 0) h->red_i[wave] = x;
+  __syncthreads();
+  int m = INT_MAX;
+  for (int w = 0; w < nw; ++w) m = min(m, h->red_i[w]);
+  __syncthreads();
+  return m;
+}
+
+// ---------------------------------------------------------------------------
+// Record view shared by all device routines.
+struct Rec {
+  const float* e;
+  const int64_t* y;
+  int64_t T;
+  int32_t V, U, S, blank;
+  int32_t stride;  // backpointer row, words
+  uint32_t* bp;
+  float* frontier;  // this record's frontier block, or nullptr
+  int64_t* labels;  // this record's output rows
+  float* scores;
+  const int16_t* ytok;
+};
+
+__device__ inline Rec make_rec(const RecordDesc& d, const Params& p, const Lds& L) {
+  Rec r;
+  r.e = d.emissions;
+  r.y = d.targets;
+  r.T = d.frames;
+  r.V = d.vocab;
+  r.U = d.tokens;
+  r.S = 2 * d.tokens + 1;
+  r.blank = d.blank;
+  r.stride = 2 * ((r.S + 31) / 32);
+  r.bp = p.bp + d.bp_offset;
+  r.frontier = d.frontier_offset >= 0 ? p.frontiers + d.frontier_offset : nullptr;
+  r.labels = p.labels + d.frame_offset;
+  r.scores = p.scores + d.frame_offset;
+  r.ytok = L.ytok;
+  return r;
+}
+
+__device__ inline int label_of(const Rec& r, int s) { return (s & 1) ? (int)r.ytok[s >> 1] : r.blank; }
+
+__device__ inline void load_tokens(const Rec& r, int16_t* ytok) {
+  for (int j = threadIdx.x; j < r.U; j += blockDim.x) ytok[j] = (int16_t)r.y[j];
+  __syncthreads();
+}
+
+// Target validation of pack_inputs (cu:852-875). Out-of-vocabulary ids are
+// rejected (status 3) even unchecked: the reference reads out of bounds there
+// (py:400-402), this build never reads outside the emission rows.
+__device__ inline int record_status(const RecordDesc& d, const Params& p, int rec, Header* h) {
+  int status = (p.validity && !p.validity[rec]) ? 2 : 0;  // cu:836
+  int oov = 0, invalid = 0, repeats = 0;
+  for (int j = threadIdx.x; j < d.tokens; j += blockDim.x) {
+    const int64_t tok = d.targets[j];
+    oov |= tok < 0 || tok >= d.vocab;
+    invalid |= tok < 0 || tok >= d.vocab || tok == d.blank;
+    repeats += j > 0 && tok == d.targets[j - 1];
+  }
+  oov = __syncthreads_or(oov);
+  if (oov) return 3;
+  if (p.check_inputs) {
+    invalid = __syncthreads_or(invalid);
+    repeats = block_sum(repeats, h);
+    if (invalid) return 3;                                  // cu:872
+    if ((int64_t)d.tokens + repeats > d.frames) return 4;   // cu:873
+  }
+  return status;
+}
+
+__device__ inline void write_failed(const Rec& r, int64_t a, int64_t b) {  // cu:650-652
+  for (int64_t t = a + threadIdx.x; t < b; t += blockDim.x) { r.labels[t] = -1; r.scores[t] = NEG_INF; }
+}
+
+// ---------------------------------------------------------------------------
+// Viterbi over frames [a, b) of one record (recurrence_impl, cu:355-523).
+struct DPOut {
+  int terminal;
+  float score;
+  int start;  // state at frame a after traceback
+};
+
+enum { TRACE_NONE = 0, TRACE_ALWAYS = 1, TRACE_IF_FINITE = 2 };
+
+template <int K>
+__device__ inline void store_bits(uint32_t* row, int tid, uint32_t bits) {
+  if constexpr (K == 4) reinterpret_cast<uint8_t*>(row)[tid] = (uint8_t)bits;
+  else if constexpr (K == 8) reinterpret_cast<uint16_t*>(row)[tid] = (uint16_t)bits;
+  else if constexpr (K == 16) row[tid] = bits;
+  else { row[2 * tid] = bits; }
+}
+
+template <int K>
+struct BitsT { using type = uint32_t; };
+template <>
+struct BitsT<32> { using type = uint64_t; };
+
+template <int K>
+__device__ inline void store_row(uint32_t* row, int tid, typename BitsT<K>::type bits) {
+  if constexpr (K == 32) {
+    row[2 * tid] = (uint32_t)bits;
+    row[2 * tid + 1] = (uint32_t)(bits >> 32);
+  } else {
+    store_bits<K>(row, tid, (uint32_t)bits);
+  }
+}
+
+// Path walk from (b-1, terminal) down to a by wave 0. Each batch loads, for up
+// to 64 frames at once (one per lane), the two backpointer words around the
+// current state, then resolves the steps serially from registers until the
+// state leaves that 32-state window. Writes labels and scores (finish,
+// cu:642-667) and returns the state at frame a.
+__device__ inline int trace_path(const Rec& r, int64_t a, int64_t b, int terminal) {
+  const int lane = threadIdx.x & 63;
+  int64_t t = b - 1;
+  int s = terminal;
+  while (t >= a) {
+    const int whi = s >> 4;
+    uint32_t vhi = 0, vlo = 0;
+    const int64_t ti = t - lane;
+    if (ti >= a) {
+      const uint32_t* row = r.bp + ti * (int64_t)r.stride;
+      vhi = row[whi];
+      if (whi > 0) vlo = row[whi - 1];
+    }
+    const int lim = (int)min((int64_t)64, t - a + 1);
+    int cur = s, steps = 0, mine = 0;
+    for (int i = 0; i < lim; ++i) {
+      const int w = cur >> 4;
+      const uint32_t hv = (uint32_t)__builtin_amdgcn_readlane((int)vhi, i);
+      const uint32_t lv = (uint32_t)__builtin_amdgcn_readlane((int)vlo, i);
+      uint32_t word;
+      if (w == whi) word = hv;
+      else if (w == whi - 1) word = lv;
+      else break;
+      if (lane == i) mine = cur;
+      cur -= (int)((word >> ((cur & 15) << 1)) & 3u);
+      steps = i + 1;
+    }
+    if (lane < steps) {
+      const int64_t tf = t - lane;
+      const int lab = label_of(r, mine);
+      r.labels[tf] = lab;
+      r.scores[tf] = r.e[tf * r.V + lab];
+    }
+    t -= steps;
+    s = cur;
+  }
+  return s;
+}
+
+template <int K, int D>
+__device__ DPOut dp_interval(const Rec& r, const Lds& L, int64_t a, int64_t b, bool record_end,
+                             const float* resume_from, int64_t start_t, float* save_frontier, int trace) {
+  using Bits = typename BitsT<K>::type;
+  Header* h = L.h;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+  const int S = r.S;
+  const int s0 = tid * K;
+  const bool active = s0 < S;
+  constexpr bool kMask = K == 32;
+  uint32_t lab[K];  // byte offset of the state's label column within a frame row
+  float skb[kMask ? 1 : K];  // 0 where the skip transition is legal, -inf elsewhere (cu:407)
+  uint32_t skm = 0;          // the same as a bit mask when K == 32
+  float al[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int s = s0 + k;
+    const int ls = s < S ? label_of(r, s) : r.blank;
+    lab[k] = 4u * (uint32_t)ls;
+    const bool ok = s >= 2 && s < S && ls != r.blank && ls != label_of(r, s - 2);
+    if constexpr (kMask) skm |= (uint32_t)ok << k;
+    else skb[k] = ok ? 0.0f : NEG_INF;
+  }
+  const float* e = r.e;
+  const int64_t V = r.V;
+  uint32_t* bp = r.bp;
+  if (resume_from) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) al[k] = (s0 + k < S) ? resume_from[s0 + k] : NEG_INF;
+  } else {
+    const float* row = e + a * V;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const float v = ldg_at(row, lab[k]);
+      al[k] = (s0 + k < S && (a > 0 || s0 + k < 2)) ? v : NEG_INF;  // cu:409
+    }
+    if (active) store_row<K>(bp + a * (int64_t)r.stride, tid, (Bits)0);  // cu:410
+    start_t = a + 1;
+  }
+  if (nwaves > 1) {
+    if (lane == 63) {
+      h->xchg[(start_t - 1) & 1][wave][0] = al[K - 2];
+      h->xchg[(start_t - 1) & 1][wave][1] = al[K - 1];
+    }
+    __syncthreads();
+  }
+  // One frame of the recurrence (cu:438-444); strict '>' keeps stay > advance >
+  // skip on ties. `evk` holds e[t][l[s]] for this thread's states.
+  auto frame = [&](int64_t t, const float (&evk)[K]) {
+    float up1 = wave_shr1(al[K - 1], NEG_INF);
+    float up2 = wave_shr1(al[K - 2], NEG_INF);
+    if (nwaves > 1 && lane == 0 && wave > 0) {
+      const int par = (int)((t - 1) & 1);
+      up2 = h->xchg[par][wave - 1][0];
+      up1 = h->xchg[par][wave - 1][1];
+    }
+    Bits bits = 0;
+#pragma unroll
+    for (int k = K - 1; k >= 0; --k) {
+      const float stay = al[k];
+      const float adv = k >= 1 ? al[k - 1] : up1;
+      const float skp = k >= 2 ? al[k - 2] : (k == 1 ? up1 : up2);
+      float best = stay;
+      Bits j = 0;
+      if (adv > best) { best = adv; j = 1; }
+      bool take;
+      if constexpr (kMask) take = ((skm >> k) & 1u) && skp > best;
+      else take = skp + skb[k] > best;
+      if (take) { best = skp; j = 2; }
+      al[k] = best + evk[k];
+      bits |= j << (2 * k);
+    }
+    if (active) store_row<K>(bp + t * (int64_t)r.stride, tid, bits);
+    if (nwaves > 1) {
+      if (lane == 63) {
+        h->xchg[t & 1][wave][0] = al[K - 2];
+        h->xchg[t & 1][wave][1] = al[K - 1];
+      }
+      __syncthreads();
+    }
+  };
+  // Prefetch ring: the gathers of frame t are issued D frames ahead; loads past
+  // the interval are clamped to its last row so every load is unconditional.
+  // The main loop runs whole groups of D frames with no exits inside a group.
+  const int64_t last = b - 1;
+  float ev[D][K];
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    const float* row = e + min(start_t + d, last) * V;
+#pragma unroll
+    for (int k = 0; k < K; ++k) ev[d][k] = ldg_at(row, lab[k]);
+  }
+  int64_t t0 = start_t;
+  for (; t0 + D <= b; t0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      frame(t0 + d, ev[d]);
+      const float* row = e + min(t0 + d + D, last) * V;
+#pragma unroll
+      for (int k = 0; k < K; ++k) ev[d][k] = ldg_at(row, lab[k]);
+    }
+  }
+  // remaining < D frames: their gathers are already in ev[0 .. b-t0-1]
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+    if (t0 + d < b) frame(t0 + d, ev[d]);
+  if (save_frontier) {  // cu:451-454
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      if (s0 + k < S) save_frontier[s0 + k] = al[k];
+  }
+  DPOut out;
+  if (record_end) {  // cu:497-500
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int s = s0 + k;
+      if (s == S - 1) h->term_v[1] = al[k];
+      if (S > 1 && s == S - 2) h->term_v[0] = al[k];
+    }
+    __syncthreads();
+    out.terminal = S - 1;
+    out.score = h->term_v[1];
+    if (S > 1 && h->term_v[0] >= h->term_v[1]) { out.terminal = S - 2; out.score = h->term_v[0]; }
+  } else {  // lowest-index argmax with the NaN-at-state-0 rule, cu:462-492
+    float bv = NEG_INF;
+    int bi = INT_MAX;
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      if (s0 + k < S) better(bv, bi, al[k], s0 + k);
+    wave_argmax(bv, bi);
+    if (lane == 0) { h->red_v[wave] = bv; h->red_i[wave] = bi; }
+    if (tid == 0) h->fbuf[0] = al[0];
+    __syncthreads();
+    bv = h->red_v[0];
+    bi = h->red_i[0];
+    for (int w = 1; w < nwaves; ++w) better(bv, bi, h->red_v[w], h->red_i[w]);
+    const float a0 = h->fbuf[0];
+    if (isnan(a0)) { bi = 0; bv = a0; }
+    out.terminal = bi;
+    out.score = bv;
+  }
+  __syncthreads();  // backpointer stores and LDS reads complete before the walk / reuse
+  out.start = 0;
+  const bool do_trace = trace == TRACE_ALWAYS || (trace == TRACE_IF_FINITE && isfinite(out.score));
+  if (do_trace) {
+    if (wave == 0) {
+      const int st = trace_path(r, a, b, out.terminal);
+      if (lane == 0) h->ibuf[0] = st;
+    }
+    __syncthreads();
+    out.start = h->ibuf[0];
+    __syncthreads();
+  }
+  return out;
+}
+
+// ---------------------------------------------------------------------------
+// Greedy shortcut for chunk [a, b) (greedy_shortcuts, cu:30-153). Returns
+// 1 when accepted (labels/scores written, *slot filled), 0 when rejected;
+// *ambiguous set when more than one legal placement exists.
+__device__ int greedy_chunk(const Rec& r, const Lds& L, int64_t a, int64_t b, Slot* slot, int* ambiguous) {
+  Header* h = L.h;
+  const int tid = threadIdx.x, NT = blockDim.x;
+  const int n = (int)(b - a);
+  const int V = r.V, blank = r.blank, S = r.S;
+  const int vw = (V + 31) >> 5;
+  // transcript alphabet (cu:53-58): blank plus every target id
+  for (int w = tid; w < vw; w += NT) L.bitmap[w] = 0;
+  __syncthreads();
+  if (tid == 0) atomicOr(&L.bitmap[blank >> 5], 1u << (blank & 31));
+  for (int j = tid; j < r.U; j += NT) {
+    const int c = r.ytok[j];
+    atomicOr(&L.bitmap[c >> 5], 1u << (c & 31));
+  }
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t acc = 0;
+    for (int w = 0; w < vw; ++w) { L.wpref[w] = acc; acc += __popc(L.bitmap[w]); }
+    h->ibuf[1] = (int)acc;
+  }
+  __syncthreads();
+  const int D = h->ibuf[1];
+  for (int c = tid; c < V; c += NT) {
+    const uint32_t word = L.bitmap[c >> 5];
+    if (word >> (c & 31) & 1u) L.sym[L.wpref[c >> 5] + __popc(word & ((1u << (c & 31)) - 1u))] = (int16_t)c;
+  }
+  __syncthreads();
+  // per-frame unique argmax over the alphabet (cu:65-91)
+  int bad = 0;
+  for (int f = tid; f < n; f += NT) {
+    const float* row = r.e + (a + f) * (int64_t)V;
+    float best = NEG_INF;
+    int chosen = -1;
+    bool dup = false;
+    for (int base = 0; base < D; base += 8) {
+      float v[8];
+      int c[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        c[q] = L.sym[min(base + q, D - 1)];
+        v[q] = row[c[q]];
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        if (base + q < D) {
+          const bool gt = v[q] > best, eq = v[q] == best;
+          best = gt ? v[q] : best;
+          chosen = gt ? c[q] : chosen;
+          dup = gt ? false : (dup || eq);
+        }
+      }
+    }
+    L.g[f] = chosen;
+    L.fs[f] = best;
+    bad |= !isfinite(best) || dup;
+  }
+  bad = __syncthreads_or(bad);
+  *ambiguous = 0;
+  if (bad) return 0;
+  // relative state walk (cu:112-117), token change points and the first token
+  int carry = 0;
+  int first = INT_MAX;
+  for (int base = 0; base < n; base += NT) {
+    const int f = base + tid;
+    int inc = 0, tc = 0;
+    if (f < n) {
+      const int x = L.g[f];
+      if (f > 0) {
+        const int w = L.g[f - 1];
+        inc = x == w ? 0 : (x == blank || w == blank ? 1 : 2);
+      }
+      tc = x != blank && (f == 0 || x != L.g[f - 1]);
+      if (x != blank) first = min(first, f);
+    }
+    const int rs = block_incl_scan(inc, h) + carry;
+    if (f < n) L.r[f] = rs;
+    // last thread's value carries into the next block of frames
+    if (tid == NT - 1) h->ibuf[2] = rs;
+    __syncthreads();
+    carry = h->ibuf[2];
+    __syncthreads();
+    (void)tc;
+  }
+  first = block_min(first, h);
+  // compact the token pattern (r, label) of change points in frame order
+  int m_total = 0;
+  for (int base = 0; base < n; base += NT) {
+    const int f = base + tid;
+    int tc = 0;
+    if (f < n) {
+      const int x = L.g[f];
+      tc = x != blank && (f == 0 || x != L.g[f - 1]);
+    }
+    const int pos = block_incl_scan(tc, h) - tc + m_total;
+    if (tc) { L.pd[pos] = L.r[f]; L.pc[pos] = L.g[f]; }
+    m_total += block_sum(tc, h);
+  }
+  const int rlast = L.r[n - 1];
+  if (tid == 0) { h->ibuf[3] = 0; h->ibuf[4] = -1; }
+  __syncthreads();
+  const bool at_start = a == 0, at_end = b == r.T;
+  if (first == INT_MAX) {
+    // all-blank chunk: even states, closed form of the placement loop (cu:119-134)
+    if (tid == 0) {
+      int matches, start = -1;
+      if (at_start && at_end) { matches = (S == 1) ? 1 : 0; start = 0; }
+      else if (at_start) { matches = 1; start = 0; }
+      else if (at_end) { matches = 1; start = S - 1; }
+      else { matches = (S + 1) / 2; start = 0; }
+      h->ibuf[3] = matches;
+      h->ibuf[4] = start;
+    }
+  } else {
+    const int c1 = L.pc[0];
+    const int r1 = L.pd[0];
+    for (int j = tid; j < r.U; j += NT) {
+      if (r.ytok[j] != c1) continue;
+      const int s = 2 * j + 1 - r1;
+      if (at_start && s > 1) continue;
+      const int terminal = s + rlast;
+      if (terminal >= S || (at_end && terminal < S - 2)) continue;
+      bool legal = true;
+      for (int i = 1; i < m_total; ++i) {
+        const int idx = j + ((L.pd[i] - r1) >> 1);
+        if (L.ytok[idx] != L.pc[i]) { legal = false; break; }
+      }
+      if (legal) { atomicAdd(&h->ibuf[3], 1); atomicExch(&h->ibuf[4], s); }
+    }
+  }
+  __syncthreads();
+  const int matches = h->ibuf[3];
+  const int start = h->ibuf[4];
+  if (matches != 1) {
+    *ambiguous = matches > 1;
+    __syncthreads();
+    return 0;
+  }
+  if (tid == 0) {  // serial fp32 chunk objective (cu:135-137)
+    float score = L.fs[0];
+    for (int f = 1; f < n; ++f) score += L.fs[f];
+    h->fbuf[1] = score;
+  }
+  __syncthreads();
+  const float score = h->fbuf[1];
+  if (!isfinite(score)) { __syncthreads(); return 0; }  // cu:139
+  for (int f = tid; f < n; f += NT) {  // finish's label/score gather collapses to g and fs here
+    r.labels[a + f] = L.g[f];
+    r.scores[a + f] = L.fs[f];
+  }
+  if (tid == 0) {
+    slot->start = start;
+    slot->end = start + rlast;
+    slot->objective = score;
+    slot->shortcut = 1;
+  }
+  __syncthreads();
+  return 1;
+}
+
+__device__ inline bool legal_seam(const Rec& r, int start, int before) {  // cu:157-161
+  const int jump = start - before;
+  return jump == 0 || jump == 1 ||
+         (jump == 2 && label_of(r, start) != r.blank && label_of(r, start) != label_of(r, start - 2));
+}
+
+// ---------------------------------------------------------------------------
+// Kernels.
+
+// One workgroup per record: statuses and diagnostics (pack_inputs, cu:819-877).
+__global__ void __launch_bounds__(256) pack_kernel(Params p) {
+  __shared__ Header hh;
+  const int rec = blockIdx.x;
+  const RecordDesc d = p.desc[rec];
+  const int status = record_status(d, p, rec, &hh);
+  if (threadIdx.x == 0) {
+    p.status[rec] = status;
+    p.objective[rec] = NEG_INF;
+    p.stitched[rec] = 0;
+    p.repair_passes[rec] = 0;
+    p.repaired_frames[rec] = 0;
+    for (int q = 0; q < 3; ++q) { p.shortcut_stats[3 * rec + q] = 0; p.routing_stats[3 * rec + q] = 0; }
+    if (p.reuse_stats)
+      for (int q = 0; q < 4; ++q) p.reuse_stats[4 * rec + q] = 0;
+    if (p.arrivals) p.arrivals[rec] = 0;
+  }
+  if (p.mode != 0) {
+    const int64_t T = d.frames;
+    const int n = (int)(1 + (T - 1) / p.H);
+    for (int c = threadIdx.x; c < n; c += blockDim.x) {  // cu:844-851
+      Slot s;
+      s.a = (int)min((int64_t)c * p.H, T);
+      s.b = (int)min((int64_t)(c + 1) * p.H, T);
+      s.flag = 1;
+      s.start = 0;
+      s.end = 0;
+      s.shortcut = 0;
+      s.frontier_end = 0;
+      s.objective = NEG_INF;
+      p.slots[d.chunk_offset + c] = s;
+    }
+  }
+}
+
+template <int K, int D>
+__global__ void __launch_bounds__(K == 32 ? 640 : 256) conventional_kernel(Params p) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  const Lds L = carve(lds_raw, p);
+  const int rec = blockIdx.x;
+  const RecordDesc d = p.desc[rec];
+  Rec r = make_rec(d, p, L);
+  const int status = record_status(d, p, rec, L.h);
+  if (threadIdx.x == 0) {
+    p.stitched[rec] = 0;
+    p.repair_passes[rec] = 0;
+    p.repaired_frames[rec] = 0;
+    for (int q = 0; q < 3; ++q) { p.shortcut_stats[3 * rec + q] = 0; p.routing_stats[3 * rec + q] = 0; }
+  }
+  if (status >= 2) {
+    if (threadIdx.x == 0) { p.status[rec] = status; p.objective[rec] = NEG_INF; }
+    write_failed(r, 0, r.T);
+    return;
+  }
+  load_tokens(r, L.ytok);
+  const DPOut o = dp_interval<K, D>(r, L, 0, r.T, true, nullptr, 1, nullptr, TRACE_IF_FINITE);
+  const bool ok = isfinite(o.score);
+  if (threadIdx.x == 0) { p.status[rec] = ok ? 0 : 1; p.objective[rec] = o.score; }  // cu:507-510
+  if (!ok) write_failed(r, 0, r.T);
+}
+
+// The record tail of optimized mode, run by the last chunk workgroup of a
+// record to finish: repair rounds, seam validation, fallback and final path.
+template <int K, int D>
+__device__ void record_tail(const Params& p, const RecordDesc& d, int rec, const Rec& r, const Lds& L) {
+  Header* h = L.h;
+  const int tid = threadIdx.x;
+  const int64_t T = r.T;
+  const int n = (int)(1 + (T - 1) / p.H);
+  Slot* gs = p.slots + d.chunk_offset;
+  Slot* sl = gs;
+  const bool in_lds = n <= p.lds_tail_slots;
+  if (in_lds) {
+    for (int c = tid; c < n; c += blockDim.x) L.tslots[c] = gs[c];
+    __syncthreads();
+    sl = L.tslots;
+  }
+  const int S = r.S;
+  const bool frontier_on = r.frontier != nullptr;
+  int64_t reuse0 = 0, reuse1 = 0, reuse2 = 0, reuse3 = 0;
+  int early = 0, rejected = 0, maxprop = 0, passes = 0;
+  int64_t repaired = 0;
+  int term = 0;
+  float fscore = NEG_INF;
+  int status = 0;
+  float objective = NEG_INF;
+  const bool repairs = p.repair_rounds > 0;
+  for (int round = 0; round < p.repair_rounds; ++round) {
+    if (tid == 0) {  // plan_repairs, cu:164-228
+      int run = !(p.overlap && early == 2);
+      if (run && p.budget > 0 && T >= p.repair_min) {
+        int before = -1;
+        int64_t begin = 0, maximum = 0;
+        bool reject = false;
+        for (int k = 0; k < n; ++k) {
+          sl[k].flag = 0;
+          if (sl[k].a >= sl[k].b) continue;
+          const bool join = before < 0 || (isfinite(sl[k].objective) && isfinite(sl[before].objective) &&
+                                           legal_seam(r, sl[k].start, sl[before].end));
+          if (join) begin = sl[k].a;
+          else {
+            maximum = max(maximum, (int64_t)sl[k].b - begin);
+            if (maximum > p.budget) reject = true;
+          }
+          before = k;
+        }
+        if (reject) {
+          ++rejected;
+          maxprop = max(maxprop, (int)maximum);
+          if (p.overlap) early = 1;
+          run = 0;
+        }
+      }
+      if (run) {
+        int previous = -1, group = -1;
+        bool merged = false;
+        for (int k = 0; k < n; ++k) {
+          if (sl[k].a >= sl[k].b) continue;
+          sl[k].flag = 0;
+          const bool join = previous < 0 || (isfinite(sl[k].objective) && isfinite(sl[previous].objective) &&
+                                             legal_seam(r, sl[k].start, sl[previous].end));
+          if (join) group = k;
+          else {
+            sl[group].b = sl[k].b;
+            sl[group].flag = 1;
+            sl[k].b = sl[k].a;
+            merged = true;
+          }
+          previous = k;
+        }
+        if (merged) {
+          ++passes;
+          for (int k = 0; k < n; ++k)
+            if (sl[k].flag) repaired += sl[k].b - sl[k].a;
+        }
+      }
+      h->ibuf[5] = early;
+    }
+    __syncthreads();
+    early = h->ibuf[5];
+    __syncthreads();
+    if (p.overlap && early) {
+      if (early == 1) {  // early full fallback (repair_recurrence, cu:535-550)
+        const Slot s0 = sl[0];
+        const bool resume = frontier_on && s0.frontier_end > 0 && s0.frontier_end <= T;
+        if (resume) { reuse1 += s0.frontier_end; reuse3 += S; }
+        const DPOut o = dp_interval<K, D>(r, L, 0, T, true, resume ? r.frontier : nullptr,
+                                          resume ? s0.frontier_end : 1, nullptr, TRACE_IF_FINITE);
+        term = o.terminal;
+        fscore = o.score;
+        status = isfinite(o.score) ? 0 : 1;
+        objective = o.score;
+        early = 2;
+        if (tid == 0) h->ibuf[5] = early;
+        __syncthreads();
+      }
+    } else {
+      for (int k = 0; k < n; ++k) {  // repair DP over merged intervals (cu:727-760)
+        const Slot s = sl[k];
+        if (s.a >= s.b || (repairs && !s.flag)) continue;
+        bool resume = false;
+        int64_t start_t = s.a + 1;
+        float* fr = frontier_on ? r.frontier + (int64_t)k * S : nullptr;
+        if (frontier_on) {
+          if (s.frontier_end > s.a && s.frontier_end <= s.b) {
+            resume = true;
+            start_t = s.frontier_end;
+            reuse0 += s.frontier_end - s.a;
+            reuse3 += S;
+          }
+          reuse2 += S;
+        }
+        const DPOut o = dp_interval<K, D>(r, L, s.a, s.b, s.b == T, resume ? fr : nullptr, start_t, fr,
+                                          TRACE_ALWAYS);
+        if (tid == 0) {
+          sl[k].objective = o.score;
+          sl[k].end = o.terminal;
+          sl[k].start = o.start;
+          if (frontier_on) sl[k].frontier_end = s.b;
+        }
+        __syncthreads();
+      }
+    }
+  }
+  int stitched = 0;
+  if (!(p.overlap && early == 2)) {  // validate_seams, cu:562-592
+    if (tid == 0) {
+      bool legal = true;
+      float total = 0.0f;
+      int previous = -1;
+      if (!repairs) { passes = 0; repaired = 0; }
+      for (int k = 0; k < n; ++k) {
+        if (repairs && sl[k].a >= sl[k].b) continue;
+        const float cost = sl[k].objective;
+        legal = legal && isfinite(cost);
+        total += cost;
+        if (previous >= 0) legal = legal && legal_seam(r, sl[k].start, sl[previous].end);
+        previous = k;
+      }
+      legal = legal && isfinite(total);
+      h->ibuf[6] = legal ? 1 : 0;
+      h->fbuf[2] = total;
+    }
+    __syncthreads();
+    stitched = h->ibuf[6];
+    status = 0;
+    objective = h->fbuf[2];
+    __syncthreads();
+    if (!stitched) {  // fallback_recurrence, cu:552-559
+      const Slot s0 = sl[0];
+      const bool resume = frontier_on && s0.frontier_end > 0 && s0.frontier_end <= T;
+      if (resume) { reuse1 += s0.frontier_end; reuse3 += S; }
+      const DPOut o = dp_interval<K, D>(r, L, 0, T, true, resume ? r.frontier : nullptr,
+                                        resume ? s0.frontier_end : 1, nullptr, TRACE_IF_FINITE);
+      term = o.terminal;
+      fscore = o.score;
+      status = isfinite(o.score) ? 0 : 1;
+      objective = o.score;
+    }
+  }
+  (void)term;
+  (void)fscore;
+  if (status != 0) write_failed(r, 0, T);
+  if (tid == 0) {
+    p.status[rec] = status;
+    p.objective[rec] = objective;
+    p.stitched[rec] = stitched;
+    p.repair_passes[rec] = passes;
+    p.repaired_frames[rec] = repaired;
+    p.routing_stats[3 * rec + 0] = early;
+    p.routing_stats[3 * rec + 1] = rejected;
+    p.routing_stats[3 * rec + 2] = maxprop;
+    if (p.reuse_stats && r.frontier) {
+      atomicAdd(reinterpret_cast<unsigned long long*>(&p.reuse_stats[4 * rec + 0]), (unsigned long long)reuse0);
+      atomicAdd(reinterpret_cast<unsigned long long*>(&p.reuse_stats[4 * rec + 1]), (unsigned long long)reuse1);
+      atomicAdd(reinterpret_cast<unsigned long long*>(&p.reuse_stats[4 * rec + 2]), (unsigned long long)reuse2);
+      atomicAdd(reinterpret_cast<unsigned long long*>(&p.reuse_stats[4 * rec + 3]), (unsigned long long)reuse3);
+    }
+  }
+}
+
+template <int K, int D>
+__global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  const Lds L = carve(lds_raw, p);
+  Header* h = L.h;
+  const int slot_index = blockIdx.x;
+  const int rec = p.slot_record[slot_index];
+  const RecordDesc d = p.desc[rec];
+  const Rec r = make_rec(d, p, L);
+  const int chunk = slot_index - d.chunk_offset;
+  const int64_t a = (int64_t)chunk * p.H;
+  const int64_t b = min(r.T, a + p.H);
+  const int status = p.status[rec];
+  if (status >= 2) {  // rejected before any label-indexed read (cu:36, cu:642-652)
+    write_failed(r, a, b);
+    return;
+  }
+  Slot* slot = p.slots + slot_index;
+  load_tokens(r, L.ytok);
+  int accepted = 0, ambiguous = 0;
+  if (p.mode == 2) accepted = greedy_chunk(r, L, a, b, slot, &ambiguous);
+  if (threadIdx.x == 0) {
+    if (accepted) {
+      atomicAdd(reinterpret_cast<unsigned long long*>(&p.shortcut_stats[3 * rec + 0]), 1ull);
+      atomicAdd(reinterpret_cast<unsigned long long*>(&p.shortcut_stats[3 * rec + 1]), (unsigned long long)(b - a));
+    } else if (ambiguous) {
+      atomicAdd(reinterpret_cast<unsigned long long*>(&p.shortcut_stats[3 * rec + 2]), 1ull);
+    }
+  }
+  if (!accepted) {  // initial chunk DP (cu:721-726), relaxed init for a > 0
+    float* fr = r.frontier ? r.frontier + (int64_t)chunk * r.S : nullptr;
+    const DPOut o = dp_interval<K, D>(r, L, a, b, b == r.T, nullptr, a + 1, fr, TRACE_ALWAYS);
+    if (threadIdx.x == 0) {
+      slot->objective = o.score;
+      slot->end = o.terminal;
+      slot->start = o.start;
+      if (fr) {
+        slot->frontier_end = (int)b;
+        atomicAdd(reinterpret_cast<unsigned long long*>(&p.reuse_stats[4 * rec + 2]), (unsigned long long)r.S);
+      }
+    }
+  }
+  // arrival: the last chunk of the record runs its tail
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __threadfence();
+    const int n = (int)(1 + (r.T - 1) / p.H);
+    const int old = atomicAdd(&p.arrivals[rec], 1);
+    h->ibuf[7] = old == n - 1;
+  }
+  __syncthreads();
+  if (!h->ibuf[7]) return;
+  __threadfence();
+  record_tail<K, D>(p, d, rec, r, L);
+}
+
+// One workgroup per record: any NaN or +inf rejects it (cu:881-891).
+__global__ void __launch_bounds__(1024) validity_kernel(const int64_t* desc, uint8_t* valid) {
+  const int rec = blockIdx.x;
+  const float* values = reinterpret_cast<const float*>(desc[2 * rec]);
+  const int64_t n = desc[2 * rec + 1];
+  int bad = 0;
+  const uintptr_t addr = reinterpret_cast<uintptr_t>(values);
+  int64_t head = (int64_t)(((16 - (addr & 15)) & 15) / 4);
+  if (head > n) head = n;
+  for (int64_t i = threadIdx.x; i < head; i += blockDim.x) {
+    const float v = values[i];
+    bad |= isnan(v) || v == INFINITY;
+  }
+  const float4* v4 = reinterpret_cast<const float4*>(values + head);
+  const int64_t n4 = (n - head) / 4;
+  for (int64_t i = threadIdx.x; i < n4; i += blockDim.x) {
+    const float4 v = v4[i];
+    bad |= isnan(v.x) || v.x == INFINITY || isnan(v.y) || v.y == INFINITY ||
+           isnan(v.z) || v.z == INFINITY || isnan(v.w) || v.w == INFINITY;
+  }
+  for (int64_t i = head + 4 * n4 + threadIdx.x; i < n; i += blockDim.x) {
+    const float v = values[i];
+    bad |= isnan(v) || v == INFINITY;
+  }
+  bad = __syncthreads_or(bad);
+  if (threadIdx.x == 0) valid[rec] = bad ? 0 : 1;
+}
+
+}  // namespace ffa
+
+// ===========================================================================
+// Host side: the C ABI of include/ffa.h.
+namespace {
+
+thread_local std::string g_error;
+thread_local hipEvent_t g_profile_start = nullptr, g_profile_stop = nullptr;
+
+int fail(int code, const std::string& message) {
+  g_error = message;
+  return code;
+}
+
+inline int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
+
+// internal[] of ffa_align_plan
+enum {
+  I_K, I_NT, I_SLOTS, I_LDS, I_UCAP, I_DCAP, I_VWORDS, I_TAILSLOTS, I_FRONTIER, I_BUDGET,
+  I_OVERLAP, I_WS_SLOTS, I_WS_ARRIVALS, I_WS_FRONTIER, I_MODE, I_H, I_FMIN, I_REPAIR_MIN
+};
+
+template <int K, int D>
+int launch_geometry(const ffa::Params& p, int NT, size_t lds, bool optimized, hipStream_t stream) {
+  hipEvent_t start = g_profile_start, stop = g_profile_stop;
+  g_profile_start = g_profile_stop = nullptr;
+  if (optimized) hipLaunchKernelGGL(ffa::pack_kernel, dim3(p.count), dim3(256), 0, stream, p);
+  if (start) hipEventRecord(start, stream);
+  if (!optimized) {
+    hipLaunchKernelGGL((ffa::conventional_kernel<K, D>), dim3(p.count), dim3(NT), lds, stream, p);
+  } else {
+    hipLaunchKernelGGL((ffa::chunk_kernel<K, D>), dim3(p.total_slots), dim3(NT), lds, stream, p);
+  }
+  if (stop) hipEventRecord(stop, stream);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(FFA_E_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
+  return FFA_OK;
+}
+
+int states_of(const ffa_record& r) { return (int)(2 * r.tokens + 1); }
+int64_t stride_of(int S) { return 2 * (((int64_t)S + 31) / 32); }
+
+// The 2-bit backpointer row of a record is 2*ceil(S/32) words; K contiguous
+// states per thread. K = 4, 8 or 16 keep a record in at most 4 waves (one per
+// SIMD); wider transcripts take K = 32 and up to 10 waves.
+void geometry(int s_max, int* K, int* NT) {
+  int k = 4;
+  while (k < 32 && (s_max + k - 1) / k > 256) k *= 2;
+  const int threads = (s_max + k - 1) / k;
+  *K = k;
+  *NT = (int)std::max<int64_t>(64, align_up(threads, 64));
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ffa_last_error(void) { return g_error.c_str(); }
+
+int ffa_profile_next_launch(hipEvent_t start, hipEvent_t stop) {
+  g_profile_start = start;
+  g_profile_stop = stop;
+  return FFA_OK;
+}
+
+void ffa_default_options(int optimized, ffa_align_options* o) {  // alignment.py:496-501
+  std::memset(o, 0, sizeof(*o));
+  o->chunk_frames = 128;
+  o->mode = optimized ? 2 : 0;
+  o->threads = 512;
+  o->repair_rounds = 2;
+  o->optimization_pass = 2;
+  o->variant = 2;
+  o->repair_budget_frames = optimized ? 512 : 0;
+  o->repair_threads = 0;
+  o->compact_alphabet = 0;
+  o->parallel_traceback = 1;
+  o->overlap_fallback = optimized ? 1 : 0;
+  o->trace_min_frames = 2048;
+  o->repair_min_frames = 2048;
+  o->frontier_reuse = optimized ? 1 : 0;
+  o->frontier_min_frames = 2048;
+  o->check_inputs = 1;
+}
+
+int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_align_options* o,
+                         ffa_align_plan* plan) {
+  using ffa::MAX_H;
+  // option checks, alignment.cu:924-941
+  if (o->frontier_min_frames < 0 || o->frontier_min_frames > INT_MAX)
+    return fail(FFA_E_INVALID, "frontier_min_frames must be a nonnegative int32");
+  if (o->repair_min_frames < 0 || o->repair_min_frames > INT_MAX)
+    return fail(FFA_E_INVALID, "repair_min_frames must be a nonnegative int32");
+  if (o->trace_min_frames <= 0 || o->trace_min_frames > INT_MAX)
+    return fail(FFA_E_INVALID, "trace_min_frames must be a positive int32");
+  if (o->overlap_fallback && o->repair_threads != 0 && o->repair_threads != o->threads)
+    return fail(FFA_E_INVALID, "overlap preserves fallback geometry");
+  if (o->repair_budget_frames < 0 || o->repair_budget_frames > INT_MAX)
+    return fail(FFA_E_INVALID, "repair budget must fit nonnegative int32");
+  if (!(o->repair_threads == 0 || o->repair_threads == 128 || o->repair_threads == 256 || o->repair_threads == 512))
+    return fail(FFA_E_INVALID, "repair threads must be 0/128/256/512");
+  if (o->variant < 0 || o->variant > 2) return fail(FFA_E_INVALID, "variant must be 0, 1, or 2");
+  if (!(o->threads == 128 || o->threads == 256 || o->threads == 512)) return fail(FFA_E_INVALID, "invalid block size");
+  if (!(o->optimization_pass == 2 || o->optimization_pass == 3))
+    return fail(FFA_E_INVALID, "optimization pass must be 2 or 3");
+  if (o->repair_rounds < 0 || o->repair_rounds > 2) return fail(FFA_E_INVALID, "invalid repair rounds");
+  if (count <= 0 || count > FFA_MAX_BATCH)
+    return fail(FFA_E_INVALID, "batch must contain 1..65535 matching emissions, targets and blanks");
+  if (o->chunk_frames <= 0 || o->chunk_frames > MAX_H || o->mode < 0 || o->mode > 2)
+    return fail(FFA_E_INVALID, "invalid chunk size or mode (chunk_frames must be 1..512)");
+  const bool optimized = o->mode != 0;
+  const int64_t H = o->chunk_frames;
+  int64_t total_frames = 0, bp_words = 0, slots = 0, frontier_floats = 0;
+  int64_t max_frames = 0, u_max = 0, v_max = 0, d_cap = 1, n_max = 0;
+  int s_max = 1;
+  for (int64_t i = 0; i < count; ++i) {
+    const ffa_record& r = records[i];
+    if (r.frames <= 0 || r.frames > INT_MAX || r.vocab <= 0 || r.vocab > FFA_MAX_VOCAB || r.tokens < 0 ||
+        2 * r.tokens + 1 > FFA_MAX_STATES || r.blank < 0 || r.blank >= r.vocab)
+      return fail(FFA_E_INVALID, "resident input shape or blank outside supported range");
+    if (!r.emissions || (r.tokens > 0 && !r.targets))
+      return fail(FFA_E_INVALID, "null emission or target pointer");
+    const int S = states_of(r);
+    total_frames += r.frames;
+    bp_words += r.frames * stride_of(S);
+    max_frames = std::max(max_frames, r.frames);
+    u_max = std::max(u_max, r.tokens);
+    v_max = std::max(v_max, r.vocab);
+    d_cap = std::max(d_cap, std::min(r.vocab, r.tokens + 1));
+    s_max = std::max(s_max, S);
+    if (optimized) {
+      const int64_t n = 1 + (r.frames - 1) / H;
+      slots += n;
+      n_max = std::max(n_max, n);
+    }
+  }
+  if (slots > INT_MAX || bp_words < 0) return fail(FFA_E_INVALID, "chunk endpoints or interval indices exceed int32 range");
+  const bool budget_on = max_frames >= o->repair_min_frames;  // alignment.cu:993-996
+  const bool frontier = optimized && o->frontier_reuse && max_frames >= o->frontier_min_frames;  // :935, :1002
+  if (frontier)
+    for (int64_t i = 0; i < count; ++i)
+      if (records[i].frames >= o->frontier_min_frames)
+        frontier_floats += (1 + (records[i].frames - 1) / H) * (int64_t)states_of(records[i]);
+  int K, NT;
+  geometry(s_max, &K, &NT);
+  const int64_t v_words = (v_max + 31) / 32;
+  const int64_t tail_slots = optimized ? std::min<int64_t>(n_max, ffa::TAIL_SLOT_CAP) : 0;
+  const int64_t greedy_bytes = optimized ? 20 * H + align_up(2 * d_cap, 16) + 8 * v_words : 0;
+  const int64_t region = std::max(greedy_bytes, 32 * tail_slots);
+  const int64_t lds = align_up((int64_t)sizeof(ffa::Header), 16) + align_up(2 * std::max<int64_t>(u_max, 1), 16) + region;
+  if (lds > 64 * 1024) return fail(FFA_E_INVALID, "batch needs more than 64 KiB of LDS per workgroup");
+  int64_t ws = align_up(4 * bp_words, 256);
+  const int64_t ws_slots = ws;
+  ws += align_up(32 * slots, 256);
+  const int64_t ws_arrivals = ws;
+  ws += optimized ? align_up(4 * count, 256) : 0;
+  const int64_t ws_frontier = ws;
+  ws += align_up(4 * frontier_floats, 256);
+  std::memset(plan, 0, sizeof(*plan));
+  plan->count = count;
+  plan->total_frames = total_frames;
+  plan->table_bytes = count * (int64_t)sizeof(ffa::RecordDesc) + 4 * slots;
+  plan->workspace_bytes = std::max<int64_t>(ws, 256);
+  plan->reuse_rows = frontier ? count : 0;
+  int64_t* in = plan->internal;
+  in[I_K] = K;
+  in[I_NT] = NT;
+  in[I_SLOTS] = slots;
+  in[I_LDS] = lds;
+  in[I_UCAP] = std::max<int64_t>(u_max, 1);
+  in[I_DCAP] = d_cap;
+  in[I_VWORDS] = v_words;
+  in[I_TAILSLOTS] = tail_slots;
+  in[I_FRONTIER] = frontier ? 1 : 0;
+  in[I_BUDGET] = budget_on ? o->repair_budget_frames : 0;
+  in[I_OVERLAP] = (budget_on && o->overlap_fallback) ? 1 : 0;
+  in[I_WS_SLOTS] = ws_slots;
+  in[I_WS_ARRIVALS] = ws_arrivals;
+  in[I_WS_FRONTIER] = ws_frontier;
+  in[I_MODE] = o->mode;
+  in[I_H] = H;
+  in[I_FMIN] = o->frontier_min_frames;
+  in[I_REPAIR_MIN] = o->repair_min_frames;
+  return FFA_OK;
+}
+
+int ffa_align_describe(const ffa_align_plan* plan, const ffa_record* records, void* host_table,
+                       int64_t host_table_bytes) {
+  if (host_table_bytes < plan->table_bytes) return fail(FFA_E_SIZE, "descriptor table buffer too small");
+  const int64_t count = plan->count;
+  const int64_t* in = plan->internal;
+  const bool optimized = in[I_MODE] != 0;
+  const bool frontier = in[I_FRONTIER] != 0;
+  const int64_t H = in[I_H];
+  auto* desc = static_cast<ffa::RecordDesc*>(host_table);
+  auto* slot_record = reinterpret_cast<int32_t*>(desc + count);
+  int64_t frame = 0, bp = 0, fr = 0;
+  int32_t slot = 0;
+  for (int64_t i = 0; i < count; ++i) {
+    const ffa_record& r = records[i];
+    const int S = states_of(r);
+    ffa::RecordDesc& d = desc[i];
+    d.emissions = r.emissions;
+    d.targets = r.targets;
+    d.frames = r.frames;
+    d.frame_offset = frame;
+    d.bp_offset = bp;
+    d.vocab = (int32_t)r.vocab;
+    d.tokens = (int32_t)r.tokens;
+    d.blank = (int32_t)r.blank;
+    d.chunk_offset = slot;
+    d.frontier_offset = -1;
+    const int64_t n = 1 + (r.frames - 1) / H;
+    if (frontier && r.frames >= in[I_FMIN]) {  // alignment.cu:374: per-record frontier storage
+      d.frontier_offset = fr;
+      fr += n * S;
+    }
+    frame += r.frames;
+    bp += r.frames * stride_of(S);
+    if (optimized) {
+      for (int64_t c = 0; c < n; ++c) slot_record[slot + c] = (int32_t)i;
+      slot += (int32_t)n;
+    }
+  }
+  return FFA_OK;
+}
+
+}  // extern "C"
+
+extern "C" int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_options* o, const void* device_table,
+                                const uint8_t* emission_validity, const ffa_align_outputs* out, void* workspace,
+                                hipStream_t stream) {
+  const int64_t* in = plan->internal;
+  const bool optimized = in[I_MODE] != 0;
+  if (!device_table || !workspace || !out->labels || !out->scores || !out->status || !out->objective ||
+      !out->stitched || !out->repair_passes || !out->repaired_frames || !out->shortcut_stats || !out->routing_stats)
+    return fail(FFA_E_INVALID, "null table, workspace or output pointer");
+  if (plan->reuse_rows > 0 && !out->reuse_stats) return fail(FFA_E_INVALID, "reuse_stats required for this plan");
+  if (o->mode != in[I_MODE] || o->chunk_frames != in[I_H]) return fail(FFA_E_INVALID, "options differ from the plan");
+  ffa::Params p{};
+  p.desc = static_cast<const ffa::RecordDesc*>(device_table);
+  p.slot_record = reinterpret_cast<const int32_t*>(p.desc + plan->count);
+  p.validity = emission_validity;
+  p.labels = out->labels;
+  p.scores = out->scores;
+  p.status = out->status;
+  p.objective = out->objective;
+  p.stitched = out->stitched;
+  p.repair_passes = out->repair_passes;
+  p.repaired_frames = out->repaired_frames;
+  p.shortcut_stats = out->shortcut_stats;
+  p.routing_stats = out->routing_stats;
+  p.reuse_stats = plan->reuse_rows > 0 ? out->reuse_stats : nullptr;
+  auto* ws = static_cast<unsigned char*>(workspace);
+  p.bp = reinterpret_cast<uint32_t*>(ws);
+  p.slots = reinterpret_cast<ffa::Slot*>(ws + in[I_WS_SLOTS]);
+  p.arrivals = optimized ? reinterpret_cast<int32_t*>(ws + in[I_WS_ARRIVALS]) : nullptr;
+  p.frontiers = reinterpret_cast<float*>(ws + in[I_WS_FRONTIER]);
+  p.budget = in[I_BUDGET];
+  p.repair_min = in[I_REPAIR_MIN];
+  p.frontier_min = in[I_FMIN];
+  p.count = (int32_t)plan->count;
+  p.total_slots = (int32_t)in[I_SLOTS];
+  p.H = (int32_t)in[I_H];
+  p.mode = (int32_t)in[I_MODE];
+  p.repair_rounds = (int32_t)o->repair_rounds;
+  p.check_inputs = o->check_inputs ? 1 : 0;
+  p.overlap = (int32_t)in[I_OVERLAP];
+  p.frontier_batch = (int32_t)in[I_FRONTIER];
+  p.u_cap = (int32_t)in[I_UCAP];
+  p.d_cap = (int32_t)in[I_DCAP];
+  p.v_words = (int32_t)in[I_VWORDS];
+  p.lds_tail_slots = (int32_t)in[I_TAILSLOTS];
+  const int NT = (int)in[I_NT];
+  const size_t lds = (size_t)in[I_LDS];
+  switch (in[I_K]) {
+    case 4: return launch_geometry<4, 8>(p, NT, lds, optimized, stream);
+    case 8: return launch_geometry<8, 6>(p, NT, lds, optimized, stream);
+    case 16: return launch_geometry<16, 4>(p, NT, lds, optimized, stream);
+    case 32: return launch_geometry<32, 1>(p, NT, lds, optimized, stream);
+    default: return fail(FFA_E_INVALID, "corrupt plan");
+  }
+}
+
+extern "C" int ffa_emission_validity_launch(const int64_t* device_descriptors, int64_t count, uint8_t* valid,
+                                            hipStream_t stream) {
+  if (count <= 0 || count > FFA_MAX_BATCH) return fail(FFA_E_INVALID, "provide 1..65535 emission tensors");
+  if (!device_descriptors || !valid) return fail(FFA_E_INVALID, "null descriptor or output pointer");
+  hipLaunchKernelGGL(ffa::validity_kernel, dim3((unsigned)count), dim3(1024), 0, stream, device_descriptors, valid);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(FFA_E_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
+  return FFA_OK;
+}

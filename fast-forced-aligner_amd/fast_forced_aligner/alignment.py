@@ -1,0 +1,242 @@
+"""Public API of the MI355X alignment path: a drop-in for the reference package.
+
+Same names, arguments, result type, statuses and error messages as the
+reference's ``src/fast_forced_aligner/alignment.py`` (cited as ``py:<line>``);
+the native operators ``fast_forced_aligner_cuda.align`` / ``.emission_validity``
+come from this package's HIP build instead of a CUDA JIT build.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from collections.abc import Sequence
+from dataclasses import dataclass
+from functools import lru_cache
+from pathlib import Path
+from typing import Literal
+
+import torch
+from torch import Tensor
+
+Mode = Literal["optimized", "conventional"]
+
+_HERE = Path(__file__).resolve().parent
+HIP_LIBRARY = _HERE / "libffa_hip.so"
+TORCH_LIBRARY = _HERE / "_ffa_torch.so"
+
+
+def _rocm_home() -> Path | None:
+    from torch.utils import cpp_extension
+
+    home = getattr(cpp_extension, "ROCM_HOME", None) or os.environ.get("ROCM_PATH")
+    return Path(home) if home else None
+
+
+@lru_cache(maxsize=1)
+def load_extension() -> None:
+    """Load the bundled HIP extension (build it first if it is absent).
+
+    Mirrors the reference loader (py:15-63) for ROCm: the libraries are built
+    in place by ``fast-forced-aligner_amd/build.py`` for gfx950; the first call
+    loads them and registers the ``fast_forced_aligner_cuda`` operators.
+    Successful calls are memoized for the process.
+
+    Raises:
+        RuntimeError: PyTorch lacks ROCm support, no AMD GPU is accessible, the
+            libraries are missing and no ROCm toolkit (hipcc) can build them,
+            or loading fails.
+    """
+    if torch.version.hip is None:
+        raise RuntimeError("fast_forced_aligner requires a ROCm-enabled PyTorch installation")
+    if not torch.cuda.is_available():
+        raise RuntimeError("fast_forced_aligner requires an accessible AMD GPU and compatible driver")
+    if not (HIP_LIBRARY.is_file() and TORCH_LIBRARY.is_file()):
+        home = _rocm_home()
+        if home is None or not (home / "bin" / "hipcc").is_file():
+            raise RuntimeError(
+                "fast_forced_aligner ships HIP source and its gfx950 libraries are not built. "
+                "Install the ROCm development toolkit (including hipcc) or run "
+                "fast-forced-aligner_amd/build.py; set ROCM_PATH if ROCm is outside /opt/rocm."
+            )
+        import importlib.util
+
+        spec = importlib.util.spec_from_file_location("_ffa_build", _HERE.parent / "build.py")
+        module = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(module)
+        module.build()
+    # the HIP library first, so the operator library resolves against it
+    ctypes.CDLL(str(HIP_LIBRARY), mode=ctypes.RTLD_GLOBAL)
+    torch.ops.load_library(str(TORCH_LIBRARY))
+
+
+@dataclass(frozen=True)
+class AlignmentBatch:
+    """Packed frame alignments and per-record diagnostics returned by ``align``.
+
+    Field meaning follows the reference (py:66-148): ``labels`` int64 ``(N,)``,
+    ``scores`` float32 ``(N,)`` (the selected input emission per frame; ``-1`` /
+    ``-inf`` for failed records), ``status`` int32 ``(B,)`` (0 ok, 1 no finite
+    path, 2 rejected by the emission mask, 3 invalid target ids, 4 insufficient
+    frames), ``objective`` float32 ``(B,)``, ``stitched``, ``repair_passes``,
+    ``repaired_frames``, ``shortcut_stats`` ``(B, 3)``, ``routing_stats``
+    ``(B, 3)`` and ``reuse_stats`` ``(B, 4)`` or ``(0, 4)``. All tensors stay on
+    the input device; reading them on the host synchronizes.
+    """
+
+    lengths: tuple[int, ...]
+    labels: Tensor
+    scores: Tensor
+    status: Tensor
+    objective: Tensor
+    stitched: Tensor
+    repair_passes: Tensor
+    repaired_frames: Tensor
+    shortcut_stats: Tensor
+    routing_stats: Tensor
+    reuse_stats: Tensor
+
+    @property
+    def paths(self) -> tuple[Tensor, ...]:
+        """Per-record views into ``labels`` (no copy, no synchronization)."""
+        return self.labels.split(self.lengths)
+
+    def raise_for_status(self) -> None:
+        """Raise if any record failed (py:163-230); reading status synchronizes.
+
+        Raises:
+            ValueError: some record has status 1, 2, 3 or 4; the message lists
+                the zero-based indices per category.
+            RuntimeError: a status outside 0..4.
+        """
+        statuses = self.status.cpu().tolist()
+        if not any(statuses):
+            return
+        unknown = [i for i, value in enumerate(statuses) if value not in (0, 1, 2, 3, 4)]
+        if unknown:
+            raise RuntimeError(f"unknown alignment status at batch indices {unknown}")
+        groups = {code: [i for i, value in enumerate(statuses) if value == code] for code in (1, 2, 3, 4)}
+        messages = []
+        for code, text in ((2, "invalid emissions at batch indices"),
+                           (1, "no finite complete CTC path for batch indices"),
+                           (3, "invalid target IDs at batch indices"),
+                           (4, "insufficient CTC frames at batch indices")):
+            if groups[code]:
+                messages.append(f"{text} {groups[code]}")
+        raise ValueError("; ".join(messages))
+
+
+def _metadata(emissions: Sequence[Tensor], targets: Sequence[Tensor],
+              blank_id: int | Sequence[int]) -> list[int]:
+    """Host-only metadata checks (py:233-252). Returns one blank per record.
+
+    The target-length limit follows the native state limit of this build
+    (2U+1 <= 20479, i.e. U <= 10239) instead of the reference's 2047.
+    """
+    count = len(emissions)
+    if not 0 < count <= 65535 or len(targets) != count:
+        raise ValueError("provide 1..65535 matching emissions and targets")
+    blanks = [blank_id] * count if type(blank_id) is int else list(blank_id)
+    if len(blanks) != count:
+        raise ValueError("provide one blank ID per record")
+    device = emissions[0].device
+    for e, t, blank in zip(emissions, targets, blanks, strict=True):
+        if (e.device.type != "cuda" or e.device != device or t.device != device
+                or e.dtype != torch.float32 or t.dtype != torch.int64
+                or e.ndim != 2 or t.ndim != 1
+                or not e.is_contiguous() or not t.is_contiguous()):
+            raise ValueError("inputs must be contiguous CUDA float32 [T,V] and int64 [U] on one device")
+        if (not 0 < e.shape[0] <= 2**31 - 1 or not 0 < e.shape[1] <= 8192
+                or t.numel() > MAX_TOKENS or type(blank) is not int or not 0 <= blank < e.shape[1]):
+            raise ValueError("unsupported frame count, vocabulary, target length, or blank ID")
+    return blanks
+
+
+MAX_TOKENS = 10239
+
+
+@torch.inference_mode()
+def validate_inputs(emissions: Sequence[Tensor], targets: Sequence[Tensor], *,
+                    blank_id: int | Sequence[int] = 0) -> None:
+    """Check metadata, target ids and CTC frame feasibility; synchronizes (py:255-309).
+
+    Raises:
+        ValueError: metadata violations, or the batch indices whose targets are
+            invalid or need more frames than available.
+    """
+    blanks = _metadata(emissions, targets, blank_id)
+    valid = []
+    for e, t, blank in zip(emissions, targets, blanks, strict=True):
+        tokens_ok = ((t >= 0) & (t < e.shape[1]) & (t != blank)).all()
+        frames_ok = t.numel() + (t[1:] == t[:-1]).sum() <= e.shape[0]
+        valid.append(tokens_ok & frames_ok)
+    failures = [i for i, ok in enumerate(torch.stack(valid).cpu().tolist()) if not ok]
+    if failures:
+        raise ValueError(f"invalid target IDs or insufficient CTC frames at batch indices {failures}")
+
+
+@torch.inference_mode()
+def emission_validity(emissions: Sequence[Tensor]) -> Tensor:
+    """Device bool mask, false for any record holding NaN or +inf (py:312-343).
+
+    No value is read by the host; the scan runs on the current stream.
+    """
+    if not 0 < len(emissions) <= 65535:
+        raise ValueError("provide 1..65535 emission tensors")
+    device = emissions[0].device
+    for e in emissions:
+        if (e.device.type != "cuda" or e.device != device or e.dtype != torch.float32
+                or e.ndim != 2 or not e.is_contiguous()
+                or not 0 < e.shape[0] <= 2**31 - 1 or not 0 < e.shape[1] <= 8192):
+            raise ValueError("emissions must be contiguous CUDA float32 [T,V] with supported dimensions on one device")
+    with torch.cuda.device(device):
+        load_extension()
+        return torch.ops.fast_forced_aligner_cuda.emission_validity(list(emissions))
+
+
+@torch.inference_mode()
+def align(emissions: Sequence[Tensor], targets: Sequence[Tensor], *,
+          blank_id: int | Sequence[int] = 0, mode: Mode = "optimized",
+          check_inputs: bool = True, emission_validity: Tensor | None = None) -> AlignmentBatch:
+    """Align known CTC targets to resident emissions on the GPU (py:346-502).
+
+    Args:
+        emissions: ``B`` contiguous float32 ``(T_i, V_i)`` device tensors.
+        targets: ``B`` contiguous int64 ``(U_i,)`` device tensors, no blanks.
+        blank_id: one int, or one int per record.
+        mode: ``"optimized"`` (128-frame chunks, greedy shortcuts, two repair
+            rounds, full-DP fallback) or ``"conventional"`` (full fp32 DP).
+        check_inputs: validate target ids and frame feasibility on the GPU.
+        emission_validity: optional device bool ``(B,)`` mask; False rejects
+            a record with status 2 unless its targets are invalid (3, 4).
+
+    Returns:
+        AlignmentBatch; failures are reported in ``status``, never raised here.
+
+    Raises:
+        ValueError: invalid mode, metadata, blank ids or mask metadata.
+        TypeError: ``check_inputs`` is not a bool.
+        RuntimeError: the HIP extension is unavailable or a launch fails.
+    """
+    if mode not in ("optimized", "conventional"):
+        raise ValueError("mode must be 'optimized' or 'conventional'")
+    if type(check_inputs) is not bool:
+        raise TypeError("check_inputs must be bool")
+    blanks = _metadata(emissions, targets, blank_id)
+    if emission_validity is not None:
+        if (not isinstance(emission_validity, Tensor)
+                or emission_validity.device != emissions[0].device
+                or emission_validity.dtype != torch.bool or emission_validity.ndim != 1
+                or emission_validity.numel() != len(emissions)
+                or not emission_validity.is_contiguous()):
+            raise ValueError("emission_validity must be contiguous CUDA bool [batch] on the input device")
+    with torch.cuda.device(emissions[0].device):
+        load_extension()
+        optimized = mode == "optimized"
+        # the fixed knob vector of py:496-501
+        tensors, lengths = torch.ops.fast_forced_aligner_cuda.align(
+            list(emissions), list(targets), blanks,
+            128, 2 if optimized else 0, 512, 2, 2, 2,
+            512 if optimized else 0, 0, False, True, optimized,
+            2048, 2048, optimized, 2048, emission_validity, check_inputs,
+        )
+    return AlignmentBatch(tuple(lengths), *tensors)

@@ -1,0 +1,143 @@
+/*
+ * fast-forced-aligner for MI355X (gfx950): C ABI of the alignment hot path.
+ *
+ * The reference exposes this path as two PyTorch operators registered in
+ * src/fast_forced_aligner/csrc/alignment.cu:1064-1070:
+ *   fast_forced_aligner_cuda::emission_validity(Tensor[] emissions) -> Tensor
+ *   fast_forced_aligner_cuda::align(Tensor[] emissions, Tensor[] targets, int[] blanks,
+ *       <knobs>, Tensor? emission_validity, bool check_inputs) -> (Tensor[], int[])
+ * This header is the same boundary with plain pointers and sizes: no torch types.
+ * The build's torch extension (csrc/ffa_torch.cpp) registers those two operators
+ * with identical schemas on top of these entry points; any other host (ctypes,
+ * cgo, a C++ server) can call them directly.
+ *
+ * Conventions
+ *   - Every pointer named "device" is HIP device memory on the current device.
+ *   - Work is enqueued on `stream`; no entry point synchronizes the host.
+ *   - Inputs are borrowed and never written. The caller keeps them alive, and
+ *     unmodified, until the stream reaches the enqueued work.
+ *   - Return value: FFA_OK, or a negative FFA_E_* code; ffa_last_error() then
+ *     returns a message (thread-local, valid until the next call on the thread).
+ */
+#ifndef FFA_H
+#define FFA_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FFA_OK 0
+#define FFA_E_INVALID (-1)   /* argument outside the supported range (reference: TORCH_CHECK) */
+#define FFA_E_HIP (-2)       /* a HIP launch or copy failed */
+#define FFA_E_SIZE (-3)      /* a caller-provided buffer is too small */
+
+#define FFA_MAX_BATCH 65535      /* alignment.cu:979, alignment.py:237 */
+#define FFA_MAX_VOCAB 8192       /* alignment.cu:970, alignment.py:249 */
+#define FFA_MAX_STATES 20479     /* 2U+1; the reference stops at 4096 (alignment.cu:970) */
+
+/* One record of the ragged batch (alignment.cu:961-988 reads the same facts
+ * from each tensor pair). */
+typedef struct ffa_record {
+  const float* emissions;  /* device, contiguous row-major [frames][vocab] fp32 */
+  const int64_t* targets;  /* device, contiguous [tokens] int64; may be NULL when tokens == 0 */
+  int64_t frames;          /* T, 1 .. INT32_MAX */
+  int64_t vocab;           /* V, 1 .. FFA_MAX_VOCAB */
+  int64_t tokens;          /* U, 2U+1 <= FFA_MAX_STATES */
+  int64_t blank;           /* 0 .. V-1 */
+} ffa_record;
+
+/* The operator's scalar arguments, same names and meaning as the schema at
+ * alignment.cu:1066-1068. The public API always passes the vector at
+ * alignment.py:496-501; ffa_default_options() returns it. */
+typedef struct ffa_align_options {
+  int64_t chunk_frames;          /* H (128); 1..512 here */
+  int64_t mode;                  /* 0 conventional, 1 chunks without greedy, 2 optimized */
+  int64_t threads;               /* 128|256|512; geometry only, validated like alignment.cu:932 */
+  int64_t repair_rounds;         /* 0..2 */
+  int64_t optimization_pass;     /* 2|3; result-identical variants */
+  int64_t variant;               /* 0..2; result-identical input addressing */
+  int64_t repair_budget_frames;  /* >= 0 */
+  int64_t repair_threads;        /* 0|128|256|512; geometry only */
+  int64_t trace_min_frames;      /* > 0; traceback strategy only */
+  int64_t repair_min_frames;     /* >= 0 */
+  int64_t frontier_min_frames;   /* >= 0 */
+  int32_t compact_alphabet;      /* result-identical */
+  int32_t parallel_traceback;    /* result-identical */
+  int32_t overlap_fallback;
+  int32_t frontier_reuse;
+  int32_t check_inputs;
+  int32_t reserved;
+} ffa_align_options;
+
+/* Sizes the caller allocates before ffa_align_launch. */
+typedef struct ffa_align_plan {
+  int64_t count;            /* B */
+  int64_t total_frames;     /* N = sum of T: length of labels and scores */
+  int64_t table_bytes;      /* descriptor table; filled on the host, copied to the device */
+  int64_t workspace_bytes;  /* device scratch for one call */
+  int64_t reuse_rows;       /* rows of reuse_stats: B when frontier reuse is active, else 0 */
+  int64_t internal[24];     /* launch geometry; read by ffa_align_launch only */
+} ffa_align_plan;
+
+/* Device output buffers: the ten tensors align() returns, in the order of
+ * alignment.cu:1059 / alignment.py:138-148. */
+typedef struct ffa_align_outputs {
+  int64_t* labels;           /* [N] */
+  float* scores;             /* [N] */
+  int32_t* status;           /* [B] */
+  float* objective;          /* [B] */
+  int32_t* stitched;         /* [B] */
+  int32_t* repair_passes;    /* [B] */
+  int64_t* repaired_frames;  /* [B] */
+  int64_t* shortcut_stats;   /* [B][3] */
+  int32_t* routing_stats;    /* [B][3] */
+  int64_t* reuse_stats;      /* [reuse_rows][4]; may be NULL when reuse_rows == 0 */
+} ffa_align_outputs;
+
+/* The knob vector of alignment.py:496-501 for mode "optimized" (nonzero) or
+ * "conventional" (zero). */
+void ffa_default_options(int optimized, ffa_align_options* options);
+
+/* Validates the batch and options like alignment.cu:924-989 and computes the
+ * buffer sizes. Host only; touches no device memory. */
+int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_align_options* options,
+                         ffa_align_plan* plan);
+
+/* Writes the descriptor table into host memory (pinned memory lets the caller
+ * upload it asynchronously, as alignment.cu:1005 does). */
+int ffa_align_describe(const ffa_align_plan* plan, const ffa_record* records,
+                       void* host_table, int64_t host_table_bytes);
+
+/* Enqueues the alignment: replaces the kernel sequence of alignment.cu:1044-1053
+ * (pack_inputs + launch_alignment). device_table holds the bytes written by
+ * ffa_align_describe; emission_validity is an optional device bool[B] mask
+ * (alignment.cu:946-952); workspace holds plan->workspace_bytes. */
+int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_options* options,
+                     const void* device_table, const uint8_t* emission_validity,
+                     const ffa_align_outputs* outputs, void* workspace, hipStream_t stream);
+
+/* Replaces emission_validity (alignment.cu:893-917 and its kernel :879-891).
+ * device_descriptors: [count][2] int64 {device address of a float array, element
+ * count}, the reference's descriptor layout. valid: device bool[count]. */
+int ffa_emission_validity_launch(const int64_t* device_descriptors, int64_t count, uint8_t* valid,
+                                 hipStream_t stream);
+
+/* Message for the last failing call on this thread. */
+const char* ffa_last_error(void);
+
+/* Measurement hook (no counterpart in the reference; for benchmarks and
+ * profilers). Arms two caller-created HIP events for the next
+ * ffa_align_launch on the calling thread: `start` is recorded on that launch's
+ * stream immediately before its dominant kernel (the full-record DP in
+ * conventional mode, the chunk kernel in optimized mode) and `stop` right
+ * after it. Passing NULL events disarms. */
+int ffa_profile_next_launch(hipEvent_t start, hipEvent_t stop);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FFA_H */

@@ -1,0 +1,186 @@
+"""CPU checks of the drop-in boundary: the C ABI library loads and exports what
+include/ffa.h declares, host-side planning validates like the reference's
+TORCH_CHECKs, the torch operators register the reference's schemas, and the
+Python API's host-side contracts (loader errors, metadata errors, status
+messages) behave like the reference's. No GPU compute runs here."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import fast_forced_aligner as ffa
+from fast_forced_aligner import alignment, capi
+
+REPO = Path(__file__).resolve().parents[1]
+HEADER = REPO / "include" / "ffa.h"
+
+REFERENCE_SCHEMAS = {
+    "emission_validity": "fast_forced_aligner_cuda::emission_validity(Tensor[] emissions) -> Tensor",
+    "align": ("fast_forced_aligner_cuda::align(Tensor[] emissions, Tensor[] targets, int[] blanks, "
+              "int chunk_frames, int mode, int threads, int repair_rounds, int optimization_pass, "
+              "int variant, int repair_budget_frames, int repair_threads, bool compact_alphabet, "
+              "bool parallel_traceback, bool overlap_fallback, int trace_min_frames, int repair_min_frames, "
+              "bool frontier_reuse, int frontier_min_frames, Tensor? emission_validity=None, "
+              "bool check_inputs=True) -> (Tensor[], int[])"),
+}
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not capi.HIP_LIBRARY.exists():
+        pytest.fail("libffa_hip.so is not built: run __graft_entry__.build()")
+    return capi.load()
+
+
+def test_header_symbols_are_exported(lib):
+    declared = set(re.findall(r"^(?:int|void|const char\*)\s+(ffa_\w+)\(", HEADER.read_text(), re.M))
+    assert declared == set(capi.EXPORTED)
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_default_options_are_the_public_knob_vector(lib):
+    o = capi.default_options(lib, True)
+    assert (o.chunk_frames, o.mode, o.threads, o.repair_rounds, o.optimization_pass, o.variant,
+            o.repair_budget_frames, o.repair_threads, o.compact_alphabet, o.parallel_traceback,
+            o.overlap_fallback, o.trace_min_frames, o.repair_min_frames, o.frontier_reuse,
+            o.frontier_min_frames, o.check_inputs) == (128, 2, 512, 2, 2, 2, 512, 0, 0, 1, 1, 2048, 2048, 1,
+                                                        2048, 1)
+    c = capi.default_options(lib, False)
+    assert (c.mode, c.repair_budget_frames, c.overlap_fallback, c.frontier_reuse) == (0, 0, 0, 0)
+
+
+def _records(shapes):
+    """Host-only records with fake (never dereferenced) device addresses."""
+    recs = (capi.Record * len(shapes))()
+    for i, (T, V, U, blank) in enumerate(shapes):
+        recs[i] = capi.Record(0x1000 * (i + 1), 0x9000 * (i + 1) if U else 0, T, V, U, blank)
+    return recs
+
+
+def _plan(lib, shapes, optimized=True, **changes):
+    o = capi.default_options(lib, optimized)
+    for k, v in changes.items():
+        setattr(o, k, v)
+    plan = capi.Plan()
+    recs = _records(shapes)
+    rc = lib.ffa_align_plan_batch(recs, len(shapes), ctypes.byref(o), ctypes.byref(plan))
+    return rc, plan, recs
+
+
+def test_plan_sizes_and_gating(lib):
+    rc, plan, recs = _plan(lib, [(500, 32, 4, 0), (320, 32, 3, 0)])
+    assert rc == 0
+    assert plan.count == 2 and plan.total_frames == 820
+    slots = 4 + 3  # ceil(T/128)
+    assert plan.table_bytes == 2 * 64 + 4 * slots
+    assert plan.reuse_rows == 0
+    rc, plan, _ = _plan(lib, [(2048, 32, 4, 0), (320, 32, 3, 0)])
+    assert rc == 0 and plan.reuse_rows == 2  # frontier reuse: batch max T >= 2048 (alignment.cu:1002)
+    rc, plan, _ = _plan(lib, [(2048, 32, 4, 0)], optimized=False)
+    assert rc == 0 and plan.reuse_rows == 0  # never in conventional mode (alignment.cu:935)
+    rc, plan, recs = _plan(lib, [(50, 8, 2, 0)])
+    buf = (ctypes.c_uint8 * (plan.table_bytes - 1))()
+    assert lib.ffa_align_describe(ctypes.byref(plan), recs, buf, plan.table_bytes - 1) == -3
+    buf = (ctypes.c_uint8 * plan.table_bytes)()
+    assert lib.ffa_align_describe(ctypes.byref(plan), recs, buf, plan.table_bytes) == 0
+    words = (ctypes.c_int64 * 8).from_buffer(buf)
+    assert (words[2], words[3]) == (50, 0)  # frames, frame offset
+
+
+@pytest.mark.parametrize("shape, changes, message", [
+    ([(0, 8, 1, 0)], {}, "shape or blank"),
+    ([(10, 0, 1, 0)], {}, "shape or blank"),
+    ([(10, 8193, 1, 0)], {}, "shape or blank"),
+    ([(10, 8, 1, 8)], {}, "shape or blank"),
+    ([(10, 8, 10240, 0)], {}, "shape or blank"),
+    ([(10, 8, 1, 0)], {"threads": 100}, "invalid block size"),
+    ([(10, 8, 1, 0)], {"repair_rounds": 3}, "invalid repair rounds"),
+    ([(10, 8, 1, 0)], {"variant": 3}, "variant must be"),
+    ([(10, 8, 1, 0)], {"optimization_pass": 4}, "optimization pass"),
+    ([(10, 8, 1, 0)], {"repair_threads": 64, "overlap_fallback": 0}, "repair threads"),
+    ([(10, 8, 1, 0)], {"repair_threads": 128}, "overlap preserves fallback geometry"),
+    ([(10, 8, 1, 0)], {"trace_min_frames": 0}, "trace_min_frames"),
+    ([(10, 8, 1, 0)], {"chunk_frames": 0}, "chunk size or mode"),
+    ([(10, 8, 1, 0)], {"mode": 3}, "chunk size or mode"),
+])
+def test_plan_rejects_like_the_reference(lib, shape, changes, message):
+    rc, _, _ = _plan(lib, shape, **changes)
+    assert rc == -1
+    assert message in lib.ffa_last_error().decode()
+
+
+def test_operator_schemas_match_the_reference():
+    torch.ops.load_library(str(alignment.TORCH_LIBRARY))
+    for name, schema in REFERENCE_SCHEMAS.items():
+        assert str(getattr(torch.ops.fast_forced_aligner_cuda, name).default._schema) == schema
+
+
+@pytest.fixture
+def fresh_loader():
+    ffa.load_extension.cache_clear()
+    yield
+    ffa.load_extension.cache_clear()
+
+
+def test_loader_requires_rocm_torch(monkeypatch, fresh_loader):
+    monkeypatch.setattr(torch.version, "hip", None)
+    with pytest.raises(RuntimeError, match="ROCm-enabled PyTorch"):
+        ffa.load_extension()
+
+
+def test_loader_requires_gpu(monkeypatch, fresh_loader):
+    monkeypatch.setattr(torch.version, "hip", "7.0")
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: False)
+    with pytest.raises(RuntimeError, match="accessible AMD GPU"):
+        ffa.load_extension()
+
+
+def test_loader_reports_missing_toolkit(monkeypatch, tmp_path, fresh_loader):
+    monkeypatch.setattr(torch.version, "hip", "7.0")
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
+    monkeypatch.setattr(alignment, "HIP_LIBRARY", tmp_path / "missing.so")
+    monkeypatch.setattr(alignment, "_rocm_home", lambda: None)
+    with pytest.raises(RuntimeError, match="including hipcc"):
+        ffa.load_extension()
+
+
+def test_metadata_errors_raise_before_native_code():
+    e = torch.zeros(12, 6)
+    t = torch.tensor([1])
+    with pytest.raises(ValueError, match="mode must be"):
+        ffa.align([e], [t], mode="unknown")
+    with pytest.raises(TypeError, match="check_inputs must be bool"):
+        ffa.align([e], [t], check_inputs=1)
+    with pytest.raises(ValueError, match="1..65535"):
+        ffa.align([], [])
+    with pytest.raises(ValueError, match="contiguous CUDA"):
+        ffa.align([e], [t])
+    with pytest.raises(ValueError, match="one blank ID per record"):
+        ffa.align([e], [t], blank_id=[0, 1])
+    with pytest.raises(ValueError):
+        ffa.emission_validity([])
+    with pytest.raises(ValueError, match="contiguous CUDA"):
+        ffa.emission_validity([e])
+
+
+def _batch(status):
+    z = torch.zeros(len(status))
+    return ffa.AlignmentBatch((1,) * len(status), z, z, torch.tensor(status, dtype=torch.int32), z, z, z, z,
+                              z, z, z)
+
+
+def test_raise_for_status_messages():
+    _batch([0, 0]).raise_for_status()
+    with pytest.raises(ValueError) as error:
+        _batch([3, 4, 2, 3, 1]).raise_for_status()
+    text = str(error.value)
+    parts = ["invalid emissions at batch indices [2]", "no finite complete CTC path for batch indices [4]",
+             "invalid target IDs at batch indices [0, 3]", "insufficient CTC frames at batch indices [1]"]
+    assert text == "; ".join(parts)
+    with pytest.raises(RuntimeError, match="unknown alignment status"):
+        _batch([0, 99]).raise_for_status()

@@ -1,0 +1,174 @@
+"""GPU parity: every output of the HIP path equals the CPU oracle, bit for bit.
+
+Labels, scores, statuses and all diagnostics are compared exactly (integer
+and index outputs bit-exact; fp32 scores/objectives compared as bit patterns,
+which is stricter than the 1e-5 relative tolerance the specification allows).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import fast_forced_aligner as ffa
+from fast_forced_aligner import capi, workloads
+from helpers import FIELDS, assert_same, collapse, golden_cases, split
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def run_gpu(emissions, targets, blank=0, mode="optimized", check_inputs=True, validity=None):
+    es = [torch.from_numpy(np.ascontiguousarray(e)).to(DEV) for e in emissions]
+    ys = [torch.from_numpy(np.ascontiguousarray(y, dtype=np.int64)).to(DEV) for y in targets]
+    mask = None if validity is None else torch.tensor(validity, dtype=torch.bool, device=DEV)
+    r = ffa.align(es, ys, blank_id=blank, mode=mode, check_inputs=check_inputs, emission_validity=mask)
+    out = {f: getattr(r, f).cpu().numpy() for f in FIELDS}
+    out["lengths"] = r.lengths
+    return out
+
+
+def compare(emissions, targets, blank=0, mode="optimized", check_inputs=True, validity=None, where=""):
+    got = run_gpu(emissions, targets, blank, mode, check_inputs, validity)
+    want = O.align(emissions, targets, blank_id=blank, mode=mode, check_inputs=check_inputs,
+                   emission_validity=validity, threads=8)
+    assert got["lengths"] == want["lengths"]
+    assert_same(got, want, where=f"{where}[{mode}] ")
+    return got
+
+
+@pytest.mark.parametrize("mode", ["conventional", "optimized"])
+def test_c1_plumbing(mode):
+    b = workloads.c1()
+    print(f"c1 {mode}", flush=True)
+    got = compare(b.emissions, b.targets, mode=mode, where="c1")
+    for p, y in zip(split(got["labels"], got["lengths"]), b.targets):
+        assert collapse(p, 0).tolist() == y.tolist()
+
+
+@pytest.mark.parametrize("mode", ["conventional", "optimized"])
+def test_golden_vectors(mode):
+    for name, e, y, blank, labels, scores in golden_cases():
+        got = run_gpu([e], [y], blank, mode)
+        if mode == "conventional" or name.startswith(("c1", "adapters", "example")):
+            np.testing.assert_array_equal(got["labels"], labels, err_msg=name)
+            np.testing.assert_array_equal(got["scores"].view(np.int32), scores.view(np.int32), err_msg=name)
+        want = O.align([e], [y], blank_id=blank, mode=mode)
+        assert_same(got, want, where=f"{name} ")
+
+
+@pytest.mark.parametrize("mode", ["conventional", "optimized"])
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_random_ragged_batches(mode, seed):
+    """Ragged batches with ties, per-record blanks, empty targets, repeats and
+    rows shorter than a chunk, over several vocabulary sizes."""
+    rng = np.random.default_rng(100 + seed)
+    es, ys, blanks = [], [], []
+    for i in range(24):
+        V = int(rng.choice([3, 6, 32, 40, 300]))
+        blank = int(rng.integers(0, V))
+        vocab = np.array([v for v in range(V) if v != blank])
+        U = int(rng.integers(0, 60))
+        y = rng.choice(vocab, U).astype(np.int64)
+        if U > 3 and i % 4 == 0:
+            y[1] = y[0]
+        R = int((y[1:] == y[:-1]).sum())
+        T = int(rng.integers(max(1, U + R), U + R + 400))
+        kind = i % 3
+        if kind == 0:
+            e = rng.integers(-4, 1, (T, V)).astype(np.float32)
+        elif kind == 1 and U:
+            e = workloads.peaky(rng, y, T, V, blank)
+        else:
+            e = np.log(rng.dirichlet(np.ones(V), T)).astype(np.float32)
+        es.append(e)
+        ys.append(y)
+        blanks.append(blank)
+    print(f"random seed {seed} {mode}", flush=True)
+    compare(es, ys, blanks, mode=mode, where=f"seed{seed}")
+
+
+@pytest.mark.parametrize("config", ["c2", "c4", "c5"])
+@pytest.mark.parametrize("mode", ["conventional", "optimized"])
+def test_config_parity(config, mode):
+    b = workloads.make(config)
+    print(f"{config} {mode}", flush=True)
+    got = compare(b.emissions, b.targets, mode=mode, where=config)
+    if config == "c5":
+        kinds = b.notes["kinds"]
+        status = got["status"]
+        assert all(s == 4 for s, k in zip(status, kinds) if k == "infeasible")
+        assert all(s == 0 for s, k in zip(status, kinds) if k != "infeasible")
+
+
+@pytest.mark.parametrize("config", ["c2", "c5"])
+def test_optimized_equals_conventional(config):
+    b = workloads.make(config)
+    opt = run_gpu(b.emissions, b.targets, mode="optimized")
+    conv = run_gpu(b.emissions, b.targets, mode="conventional")
+    np.testing.assert_array_equal(opt["labels"], conv["labels"])
+    np.testing.assert_array_equal(opt["scores"], conv["scores"])
+    np.testing.assert_array_equal(opt["status"], conv["status"])
+
+
+def test_unchecked_inputs_and_mask():
+    rng = np.random.default_rng(5)
+    es = [np.log(rng.dirichlet(np.ones(6), n)).astype(np.float32) for n in (7, 257, 130)]
+    ys = [np.array([1, 1, 2]), np.array([2, 3]), np.array([1, 1])]
+    es[2][:] = 0
+    for mode in ("conventional", "optimized"):
+        compare(es, ys, mode=mode, check_inputs=False, where="unchecked")
+        compare(es, ys, mode=mode, validity=[True, False, True], where="mask")
+
+
+def test_c_abi_direct_call():
+    """Drive the HIP library through its C entry points (ctypes), with caller-
+    allocated device buffers, and compare with the oracle."""
+    lib = capi.load()
+    b = workloads.c1()
+    es = [torch.from_numpy(e).to(DEV) for e in b.emissions]
+    ys = [torch.from_numpy(y).to(DEV) for y in b.targets]
+    recs = (capi.Record * 2)()
+    for i, (e, y) in enumerate(zip(es, ys)):
+        recs[i] = capi.Record(e.data_ptr(), y.data_ptr(), e.shape[0], e.shape[1], y.numel(), 0)
+    for optimized in (False, True):
+        o = capi.default_options(lib, optimized)
+        plan = capi.Plan()
+        capi.check(lib, lib.ffa_align_plan_batch(recs, 2, ctypes.byref(o), ctypes.byref(plan)))
+        host = torch.empty(plan.table_bytes, dtype=torch.uint8).pin_memory()
+        capi.check(lib, lib.ffa_align_describe(ctypes.byref(plan), recs, host.data_ptr(), plan.table_bytes))
+        table = host.to(DEV)
+        N, B = plan.total_frames, 2
+        outs = {"labels": torch.empty(N, dtype=torch.int64, device=DEV),
+                "scores": torch.empty(N, dtype=torch.float32, device=DEV),
+                "status": torch.empty(B, dtype=torch.int32, device=DEV),
+                "objective": torch.empty(B, dtype=torch.float32, device=DEV),
+                "stitched": torch.empty(B, dtype=torch.int32, device=DEV),
+                "repair_passes": torch.empty(B, dtype=torch.int32, device=DEV),
+                "repaired_frames": torch.empty(B, dtype=torch.int64, device=DEV),
+                "shortcut_stats": torch.empty(B, 3, dtype=torch.int64, device=DEV),
+                "routing_stats": torch.empty(B, 3, dtype=torch.int32, device=DEV),
+                "reuse_stats": torch.empty(plan.reuse_rows, 4, dtype=torch.int64, device=DEV)}
+        out = capi.Outputs(*[outs[f].data_ptr() if outs[f].numel() else None for f in FIELDS])
+        ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=DEV)
+        stream = torch.cuda.current_stream().cuda_stream
+        capi.check(lib, lib.ffa_align_launch(ctypes.byref(plan), ctypes.byref(o), table.data_ptr(), None,
+                                             ctypes.byref(out), ws.data_ptr(), stream))
+        torch.cuda.synchronize()
+        got = {f: outs[f].cpu().numpy() for f in FIELDS}
+        want = O.align(b.emissions, b.targets, mode="optimized" if optimized else "conventional")
+        assert_same(got, want, where="capi ")
+
+
+def test_emission_validity_scan():
+    rng = np.random.default_rng(9)
+    es = [np.log(rng.dirichlet(np.ones(7), n)).astype(np.float32) for n in (1, 5, 257, 3000)]
+    es[1][2, 3] = np.nan
+    es[2][0, 0] = np.inf
+    es[3][-1, -1] = -np.inf
+    mask = ffa.emission_validity([torch.from_numpy(e).to(DEV) for e in es])
+    assert mask.dtype == torch.bool
+    assert mask.cpu().tolist() == [O.emission_valid(e) for e in es] == [True, False, False, True]
