@@ -10,12 +10,13 @@
 //     2-bit backpointers in HBM, picks the terminal, walks the path back and
 //     writes labels and scores (cu:919-1061 sequence pack -> recurrence -> finish).
 //   optimized mode: two launches.
-//     pack_kernel: one workgroup per record: statuses, diagnostics, chunk slots.
-//     chunk_kernel: one workgroup per 128-frame chunk: greedy shortcut
-//       (cu:30-153) or relaxed chunk DP (cu:355-523) writes the chunk's labels
-//       and scores directly; the last chunk of a record to finish (atomic
-//       arrival counter) runs the record tail: repair planning (cu:164-228),
-//       repair DP, seam validation (cu:562-592), full-DP fallback and its path.
+//     chunk_kernel: one workgroup per 128-frame chunk. It stages and validates
+//       the record's targets, then takes the greedy shortcut (cu:30-153) or
+//       runs the relaxed chunk DP (cu:355-523), writing the chunk's labels and
+//       scores directly plus a slot with its endpoints and objective.
+//     tail_kernel: one workgroup per record: repair planning (cu:164-228),
+//       repair DP, seam validation (cu:562-592), full-DP fallback with its
+//       path, and all per-record outputs.
 //
 // DP layout: a workgroup of NT = 64*W threads owns the 2L+1 states of one
 // record, K contiguous states per thread (state s = tid*K + k). The s-1 / s-2
@@ -55,8 +56,12 @@ struct RecordDesc {  // device descriptor table entry, 64 bytes
 static_assert(sizeof(RecordDesc) == 64, "descriptor layout");
 
 struct Slot {  // per-chunk state of optimized mode (cu:1021-1029 buffers), 32 bytes
-  int32_t a, b, flag, start, end, shortcut, frontier_end;
+  int32_t a, b, start, end, frontier_end;
   float objective;
+  int16_t flag;    // merged-interval flag of the repair rounds
+  int16_t kind;    // 0 chunk DP, 1 greedy shortcut, 2 chunk DP after an ambiguous placement
+  int16_t status;  // record status seen by the chunk (>= 2: rejected)
+  int16_t reserved;
 };
 static_assert(sizeof(Slot) == 32, "slot layout");
 
@@ -76,7 +81,6 @@ struct Params {
   int64_t* reuse_stats;
   uint32_t* bp;
   Slot* slots;
-  int32_t* arrivals;
   float* frontiers;
   int64_t budget, repair_min, frontier_min;
   int32_t count, total_slots, H, mode, repair_rounds, check_inputs, overlap, frontier_batch;
@@ -90,6 +94,8 @@ struct Header {
   float xchg[2][16][2];  // DP neighbour values crossing wave boundaries
   float red_v[16];
   int red_i[16];
+  int red_j[16];
+  uint32_t red_m[16];
   float term_v[2];
   int ibuf[8];
   float fbuf[4];
@@ -107,6 +113,8 @@ struct Lds {
   int16_t* sym;
   uint32_t* bitmap;
   uint32_t* wpref;
+  int32_t* cand;
+  int32_t* candok;
   Slot* tslots;
 };
 
@@ -121,11 +129,14 @@ __device__ inline Lds carve(unsigned char* base, const Params& p) {
   off = align16(off + 2 * (size_t)p.u_cap);
   unsigned char* region = base + off;
   size_t g = 0;
-  L.g = reinterpret_cast<int32_t*>(region + g); g += 4 * (size_t)p.H;
-  L.fs = reinterpret_cast<float*>(region + g); g += 4 * (size_t)p.H;
-  L.r = reinterpret_cast<int32_t*>(region + g); g += 4 * (size_t)p.H;
-  L.pd = reinterpret_cast<int32_t*>(region + g); g += 4 * (size_t)p.H;
-  L.pc = reinterpret_cast<int32_t*>(region + g); g += 4 * (size_t)p.H;
+  const size_t h32 = (size_t)((p.H + 31) & ~31);
+  L.g = reinterpret_cast<int32_t*>(region + g); g += 4 * h32;
+  L.fs = reinterpret_cast<float*>(region + g); g += 4 * h32;
+  L.r = reinterpret_cast<int32_t*>(region + g); g += 4 * h32;
+  L.pd = reinterpret_cast<int32_t*>(region + g); g += 4 * h32;
+  L.pc = reinterpret_cast<int32_t*>(region + g); g += 4 * h32;
+  L.cand = reinterpret_cast<int32_t*>(region + g); g += 4 * 256;
+  L.candok = reinterpret_cast<int32_t*>(region + g); g += 4 * 256;
   L.sym = reinterpret_cast<int16_t*>(region + g); g = align16(g + 2 * (size_t)p.d_cap);
   L.bitmap = reinterpret_cast<uint32_t*>(region + g); g += 4 * (size_t)p.v_words;
   L.wpref = reinterpret_cast<uint32_t*>(region + g);
@@ -146,6 +157,50 @@ __device__ inline float wave_shr1(float x, float fill) {
   // DPP wave_shr:1 - lane i receives lane i-1; lane 0 keeps `fill`.
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
       __builtin_bit_cast(int, fill), __builtin_bit_cast(int, x), 0x138, 0xf, 0xf, false));
+}
+
+template <int CTRL, int ROW_MASK>
+__device__ inline int dpp_add(int v) {
+  return v + __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, false);
+}
+
+// Wave64 inclusive scan: row_shr 1/2/4/8 inside rows of 16 lanes, then
+// row_bcast:15 and row_bcast:31 carry row totals forward (six DPP adds).
+__device__ inline int wave_scan_dpp(int x) {
+  x = dpp_add<0x111, 0xf>(x);
+  x = dpp_add<0x112, 0xf>(x);
+  x = dpp_add<0x114, 0xf>(x);
+  x = dpp_add<0x118, 0xf>(x);
+  x = dpp_add<0x142, 0xa>(x);
+  x = dpp_add<0x143, 0xc>(x);
+  return x;
+}
+
+__device__ inline int wave_shr1_int(int x, int fill) {
+  return __builtin_amdgcn_update_dpp(fill, x, 0x138, 0xf, 0xf, false);
+}
+
+__device__ inline float readlane_f(float x, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
+}
+
+__device__ inline uint32_t lanes_below(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+// Sequential fp32 sum ((x0 + x1) + x2) + ... of an LDS array by one thread,
+// reading 32 values ahead of the dependent adds. x must hold a multiple of 32.
+__device__ inline float serial_sum(const float* x, int n) {
+  float acc = x[0];
+  for (int base = 0; base < n; base += 32) {
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] = x[base + i];
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+      if (base + i >= 1 && base + i < n) acc += v[i];
+  }
+  return acc;
 }
 
 // argmax with the reference's comparator (value desc, state asc; NaN never wins),
@@ -251,29 +306,6 @@ __device__ inline int label_of(const Rec& r, int s) { return (s & 1) ? (int)r.yt
 __device__ inline void load_tokens(const Rec& r, int16_t* ytok) {
   for (int j = threadIdx.x; j < r.U; j += blockDim.x) ytok[j] = (int16_t)r.y[j];
   __syncthreads();
-}
-
-// Target validation of pack_inputs (cu:852-875). Out-of-vocabulary ids are
-// rejected (status 3) even unchecked: the reference reads out of bounds there
-// (py:400-402), this build never reads outside the emission rows.
-__device__ inline int record_status(const RecordDesc& d, const Params& p, int rec, Header* h) {
-  int status = (p.validity && !p.validity[rec]) ? 2 : 0;  // cu:836
-  int oov = 0, invalid = 0, repeats = 0;
-  for (int j = threadIdx.x; j < d.tokens; j += blockDim.x) {
-    const int64_t tok = d.targets[j];
-    oov |= tok < 0 || tok >= d.vocab;
-    invalid |= tok < 0 || tok >= d.vocab || tok == d.blank;
-    repeats += j > 0 && tok == d.targets[j - 1];
-  }
-  oov = __syncthreads_or(oov);
-  if (oov) return 3;
-  if (p.check_inputs) {
-    invalid = __syncthreads_or(invalid);
-    repeats = block_sum(repeats, h);
-    if (invalid) return 3;                                  // cu:872
-    if ((int64_t)d.tokens + repeats > d.frames) return 4;   // cu:873
-  }
-  return status;
 }
 
 __device__ inline void write_failed(const Rec& r, int64_t a, int64_t b) {  // cu:650-652
@@ -514,151 +546,243 @@ __device__ DPOut dp_interval(const Rec& r, const Lds& L, int64_t a, int64_t b, b
 }
 
 // ---------------------------------------------------------------------------
-// Greedy shortcut for chunk [a, b) (greedy_shortcuts, cu:30-153). Returns
-// 1 when accepted (labels/scores written, *slot filled), 0 when rejected;
-// *ambiguous set when more than one legal placement exists.
+// Target staging and validation (pack_inputs, cu:819-877), done by every
+// workgroup that needs the record: copies the targets into LDS as int16,
+// computes the status and the transcript alphabet (cu:53-58). For V <= 32 the
+// alphabet is returned as a bit mask; otherwise it is left in L.bitmap.
+// Out-of-vocabulary ids are rejected (status 3) even unchecked: the reference
+// reads out of bounds there (py:400-402); this build never reads outside the
+// emission rows.
+struct Staged {
+  int status;
+  uint32_t alpha32;
+};
+
+enum { ALPHABET_NONE = 0, ALPHABET_MASK32 = 1, ALPHABET_BITMAP = 2 };
+
+__device__ Staged stage_tokens(const RecordDesc& d, const Params& p, int rec, const Lds& L, int alphabet) {
+  Header* h = L.h;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+  const int V = d.vocab;
+  if (alphabet == ALPHABET_BITMAP) {
+    for (int w = tid; w < (V + 31) / 32; w += blockDim.x) L.bitmap[w] = 0;
+    __syncthreads();
+    if (tid == 0) atomicOr(&L.bitmap[d.blank >> 5], 1u << (d.blank & 31));
+  }
+  int oov = 0, invalid = 0, repeats = 0;
+  uint32_t mask = 0;
+  for (int j = tid; j < d.tokens; j += blockDim.x) {
+    const int64_t tok = d.targets[j];
+    const bool out = tok < 0 || tok >= V;  // checked as int64 before narrowing (cu:860)
+    oov |= out;
+    invalid |= out || tok == d.blank;
+    repeats += j > 0 && tok == d.targets[j - 1];  // cu:861
+    L.ytok[j] = (int16_t)(out ? 0 : tok);
+    if (!out) {
+      if (alphabet == ALPHABET_BITMAP) atomicOr(&L.bitmap[tok >> 5], 1u << (tok & 31));
+      else if (alphabet == ALPHABET_MASK32) mask |= 1u << tok;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {  // one reduction for all four values
+    oov |= __shfl_xor(oov, off, 64);
+    invalid |= __shfl_xor(invalid, off, 64);
+    repeats += __shfl_xor(repeats, off, 64);
+    mask |= (uint32_t)__shfl_xor((int)mask, off, 64);
+  }
+  if (lane == 0) {
+    h->red_i[wave] = oov | (invalid << 1);
+    h->red_j[wave] = repeats;
+    h->red_m[wave] = mask;
+  }
+  __syncthreads();
+  int flags = 0, reps = 0;
+  uint32_t m = alphabet == ALPHABET_MASK32 ? 1u << d.blank : 0u;
+  for (int w = 0; w < nw; ++w) {
+    flags |= h->red_i[w];
+    reps += h->red_j[w];
+    m |= h->red_m[w];
+  }
+  __syncthreads();
+  Staged st;
+  st.alpha32 = m;
+  if (flags & 1) st.status = 3;
+  else if (p.check_inputs && (flags & 2)) st.status = 3;                          // cu:872
+  else if (p.check_inputs && (int64_t)d.tokens + reps > d.frames) st.status = 4;  // cu:873
+  else st.status = (p.validity && !p.validity[rec]) ? 2 : 0;                     // cu:836
+  return st;
+}
+
+__device__ inline bool legal_seam(const Rec& r, int start, int before) {  // cu:157-161
+  const int jump = start - before;
+  return jump == 0 || jump == 1 ||
+         (jump == 2 && label_of(r, start) != r.blank && label_of(r, start) != label_of(r, start - 2));
+}
+
+// ---------------------------------------------------------------------------
+// Greedy shortcut for chunk [a, b) (greedy_shortcuts, cu:30-153).
+//
+// Per frame: the unique maximum over the transcript alphabet (ties or a
+// non-finite maximum reject the chunk). The greedy labels define a relative
+// state walk r (0 same label, 1 when a blank is involved, 2 token to token).
+// The token change points form a pattern c_1..c_m; a start state s is a legal
+// placement iff the pattern equals the contiguous target substring
+// y[j .. j+m) (s = 2j+1-r(first token)), plus the start/end constraints of the
+// reference's placement loop. This is exactly the set the reference's O(S*H)
+// loop accepts; here candidates are prefiltered on three tokens and the rest
+// is checked with one comparison per (candidate, position) pair.
+//
+// Returns 1 when accepted (labels and scores written, *slot filled);
+// *ambiguous is set when more than one placement is legal.
+constexpr int CAND_CAP = 256;
+
 __device__ int greedy_chunk(const Rec& r, const Lds& L, int64_t a, int64_t b, Slot* slot, int* ambiguous) {
   Header* h = L.h;
   const int tid = threadIdx.x, NT = blockDim.x;
   const int n = (int)(b - a);
-  const int V = r.V, blank = r.blank, S = r.S;
-  const int vw = (V + 31) >> 5;
-  // transcript alphabet (cu:53-58): blank plus every target id
-  for (int w = tid; w < vw; w += NT) L.bitmap[w] = 0;
-  __syncthreads();
-  if (tid == 0) atomicOr(&L.bitmap[blank >> 5], 1u << (blank & 31));
-  for (int j = tid; j < r.U; j += NT) {
-    const int c = r.ytok[j];
-    atomicOr(&L.bitmap[c >> 5], 1u << (c & 31));
-  }
-  __syncthreads();
-  if (tid == 0) {
-    uint32_t acc = 0;
-    for (int w = 0; w < vw; ++w) { L.wpref[w] = acc; acc += __popc(L.bitmap[w]); }
-    h->ibuf[1] = (int)acc;
-  }
-  __syncthreads();
-  const int D = h->ibuf[1];
-  for (int c = tid; c < V; c += NT) {
-    const uint32_t word = L.bitmap[c >> 5];
-    if (word >> (c & 31) & 1u) L.sym[L.wpref[c >> 5] + __popc(word & ((1u << (c & 31)) - 1u))] = (int16_t)c;
-  }
-  __syncthreads();
-  // per-frame unique argmax over the alphabet (cu:65-91)
+  const int V = r.V, blank = r.blank, S = r.S, U = r.U;
   int bad = 0;
-  for (int f = tid; f < n; f += NT) {
-    const float* row = r.e + (a + f) * (int64_t)V;
-    float best = NEG_INF;
-    int chosen = -1;
-    bool dup = false;
-    for (int base = 0; base < D; base += 8) {
-      float v[8];
-      int c[8];
+  {
+    // general vocabulary: compact symbol list, then gathered loads per frame
+    const int vw = (V + 31) >> 5;
+    if (tid == 0) {
+      uint32_t acc = 0;
+      for (int w = 0; w < vw; ++w) { L.wpref[w] = acc; acc += __popc(L.bitmap[w]); }
+      h->ibuf[1] = (int)acc;
+    }
+    __syncthreads();
+    const int D = h->ibuf[1];
+    for (int c = tid; c < V; c += NT) {
+      const uint32_t word = L.bitmap[c >> 5];
+      if (word >> (c & 31) & 1u) L.sym[L.wpref[c >> 5] + __popc(word & ((1u << (c & 31)) - 1u))] = (int16_t)c;
+    }
+    __syncthreads();
+    for (int f = tid; f < n; f += NT) {
+      const float* row = r.e + (a + f) * (int64_t)V;
+      float best = NEG_INF;
+      int chosen = -1;
+      bool dup = false;
+      for (int base = 0; base < D; base += 8) {
+        float v[8];
+        int c[8];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        c[q] = L.sym[min(base + q, D - 1)];
-        v[q] = row[c[q]];
-      }
+        for (int q = 0; q < 8; ++q) {
+          c[q] = L.sym[min(base + q, D - 1)];
+          v[q] = ldg_at(row, 4u * (uint32_t)c[q]);
+        }
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        if (base + q < D) {
-          const bool gt = v[q] > best, eq = v[q] == best;
-          best = gt ? v[q] : best;
-          chosen = gt ? c[q] : chosen;
-          dup = gt ? false : (dup || eq);
+        for (int q = 0; q < 8; ++q) {
+          if (base + q < D) {
+            const bool gt = v[q] > best, eq = v[q] == best;
+            best = gt ? v[q] : best;
+            chosen = gt ? c[q] : chosen;
+            dup = gt ? false : (dup || eq);
+          }
         }
       }
+      L.g[f] = chosen;
+      L.fs[f] = best;
+      bad |= !isfinite(best) || dup;
     }
-    L.g[f] = chosen;
-    L.fs[f] = best;
-    bad |= !isfinite(best) || dup;
   }
   bad = __syncthreads_or(bad);
   *ambiguous = 0;
-  if (bad) return 0;
-  // relative state walk (cu:112-117), token change points and the first token
+  if (bad) { __syncthreads(); return 0; }
+  // relative walk and token pattern in one scan: low 16 bits r, high 16 bits
+  // the running count of token change points
   int carry = 0;
-  int first = INT_MAX;
   for (int base = 0; base < n; base += NT) {
     const int f = base + tid;
-    int inc = 0, tc = 0;
+    int inc = 0, tc = 0, x = 0;
     if (f < n) {
-      const int x = L.g[f];
-      if (f > 0) {
-        const int w = L.g[f - 1];
-        inc = x == w ? 0 : (x == blank || w == blank ? 1 : 2);
-      }
-      tc = x != blank && (f == 0 || x != L.g[f - 1]);
-      if (x != blank) first = min(first, f);
+      x = L.g[f];
+      const int w = f > 0 ? L.g[f - 1] : -1;
+      if (f > 0) inc = x == w ? 0 : (x == blank || w == blank ? 1 : 2);
+      tc = x != blank && (f == 0 || x != w);
     }
-    const int rs = block_incl_scan(inc, h) + carry;
-    if (f < n) L.r[f] = rs;
-    // last thread's value carries into the next block of frames
-    if (tid == NT - 1) h->ibuf[2] = rs;
+    const int v = block_incl_scan(inc | (tc << 16), h) + carry;
+    if (f < n) {
+      L.r[f] = v & 0xffff;
+      if (tc) {
+        const int pos = (v >> 16) - 1;
+        L.pc[pos] = x;
+        L.pd[pos] = v & 0xffff;
+      }
+    }
+    if (tid == NT - 1) h->ibuf[2] = v;
     __syncthreads();
     carry = h->ibuf[2];
     __syncthreads();
-    (void)tc;
   }
-  first = block_min(first, h);
-  // compact the token pattern (r, label) of change points in frame order
-  int m_total = 0;
-  for (int base = 0; base < n; base += NT) {
-    const int f = base + tid;
-    int tc = 0;
-    if (f < n) {
-      const int x = L.g[f];
-      tc = x != blank && (f == 0 || x != L.g[f - 1]);
-    }
-    const int pos = block_incl_scan(tc, h) - tc + m_total;
-    if (tc) { L.pd[pos] = L.r[f]; L.pc[pos] = L.g[f]; }
-    m_total += block_sum(tc, h);
-  }
+  const int m = carry >> 16;
   const int rlast = L.r[n - 1];
-  if (tid == 0) { h->ibuf[3] = 0; h->ibuf[4] = -1; }
-  __syncthreads();
   const bool at_start = a == 0, at_end = b == r.T;
-  if (first == INT_MAX) {
+  int matches = 0, start = -1;
+  if (m == 0) {
     // all-blank chunk: even states, closed form of the placement loop (cu:119-134)
-    if (tid == 0) {
-      int matches, start = -1;
-      if (at_start && at_end) { matches = (S == 1) ? 1 : 0; start = 0; }
-      else if (at_start) { matches = 1; start = 0; }
-      else if (at_end) { matches = 1; start = S - 1; }
-      else { matches = (S + 1) / 2; start = 0; }
-      h->ibuf[3] = matches;
-      h->ibuf[4] = start;
-    }
+    if (at_start && at_end) { matches = (S == 1) ? 1 : 0; start = 0; }
+    else if (at_start) { matches = 1; start = 0; }
+    else if (at_end) { matches = 1; start = S - 1; }
+    else { matches = (S + 1) / 2; start = 0; }
   } else {
-    const int c1 = L.pc[0];
     const int r1 = L.pd[0];
-    for (int j = tid; j < r.U; j += NT) {
-      if (r.ytok[j] != c1) continue;
+    const int pre = min(m, 3);
+    // placement constraints of cu:119-123 for target position j (state s = 2j+1-r1)
+    auto placeable = [&](int j) {
       const int s = 2 * j + 1 - r1;
-      if (at_start && s > 1) continue;
       const int terminal = s + rlast;
-      if (terminal >= S || (at_end && terminal < S - 2)) continue;
-      bool legal = true;
-      for (int i = 1; i < m_total; ++i) {
-        const int idx = j + ((L.pd[i] - r1) >> 1);
-        if (L.ytok[idx] != L.pc[i]) { legal = false; break; }
-      }
-      if (legal) { atomicAdd(&h->ibuf[3], 1); atomicExch(&h->ibuf[4], s); }
+      return !((at_start && s > 1) || terminal >= S || (at_end && terminal < S - 2));
+    };
+    if (tid == 0) h->ibuf[3] = 0;
+    __syncthreads();
+    for (int j = tid; j + m <= U; j += NT) {  // prefilter on the first three pattern tokens
+      bool hit = L.ytok[j] == L.pc[0];
+      for (int i = 1; i < pre && hit; ++i) hit = L.ytok[j + i] == L.pc[i];
+      if (!hit || !placeable(j)) continue;
+      const int k = atomicAdd(&h->ibuf[3], 1);
+      if (k < CAND_CAP) { L.cand[k] = j; L.candok[k] = 1; }
     }
+    __syncthreads();
+    const int total = h->ibuf[3];
+    if (total <= CAND_CAP) {
+      const int width = m - pre;  // remaining positions, one comparison per (candidate, position)
+      for (int q = tid; q < total * width; q += NT) {
+        const int ci = q / width, i = pre + q % width;
+        if (L.ytok[L.cand[ci] + i] != L.pc[i]) L.candok[ci] = 0;
+      }
+      __syncthreads();
+      int local = 0, mine = -1;
+      for (int ci = tid; ci < total; ci += NT)
+        if (L.candok[ci]) { ++local; mine = L.cand[ci]; }
+      matches = block_sum(local, h);
+      if (local) h->ibuf[4] = 2 * mine + 1 - r1;
+      __syncthreads();
+      start = h->ibuf[4];
+    } else {
+      // more prefiltered candidates than the list holds: exact serial scan
+      // (no realistic transcript repeats a three-token prefix this often)
+      if (tid == 0) {
+        int count = 0, found = -1;
+        for (int j = 0; j + m <= U && count < 2; ++j) {
+          bool hit = placeable(j);
+          for (int i = 0; i < m && hit; ++i) hit = L.ytok[j + i] == L.pc[i];
+          if (hit) { ++count; found = 2 * j + 1 - r1; }
+        }
+        h->ibuf[3] = count;
+        h->ibuf[4] = found;
+      }
+      __syncthreads();
+      matches = h->ibuf[3];
+      start = h->ibuf[4];
+    }
+    __syncthreads();
   }
-  __syncthreads();
-  const int matches = h->ibuf[3];
-  const int start = h->ibuf[4];
   if (matches != 1) {
     *ambiguous = matches > 1;
     __syncthreads();
     return 0;
   }
-  if (tid == 0) {  // serial fp32 chunk objective (cu:135-137)
-    float score = L.fs[0];
-    for (int f = 1; f < n; ++f) score += L.fs[f];
-    h->fbuf[1] = score;
-  }
+  if (tid == 0) h->fbuf[1] = serial_sum(L.fs, n);  // serial fp32 chunk objective (cu:135-137)
   __syncthreads();
   const float score = h->fbuf[1];
   if (!isfinite(score)) { __syncthreads(); return 0; }  // cu:139
@@ -670,55 +794,155 @@ __device__ int greedy_chunk(const Rec& r, const Lds& L, int64_t a, int64_t b, Sl
     slot->start = start;
     slot->end = start + rlast;
     slot->objective = score;
-    slot->shortcut = 1;
   }
   __syncthreads();
   return 1;
 }
 
-__device__ inline bool legal_seam(const Rec& r, int start, int before) {  // cu:157-161
-  const int jump = start - before;
-  return jump == 0 || jump == 1 ||
-         (jump == 2 && label_of(r, start) != r.blank && label_of(r, start) != label_of(r, start - 2));
+
+// Greedy shortcut of one chunk (at most 128 frames, V <= 32) by wave 0 alone,
+// with no workgroup barrier: lane l owns frames a+l and a+64+l, whose rows are
+// already in registers. Same decisions as greedy_chunk; the pattern scan uses
+// DPP, candidates are compacted with ballots, and the fp32 chunk objective is
+// a readlane chain in frame order. Other waves only wait for the verdict.
+__device__ int greedy_wave(const Rec& r, const Lds& L, int64_t a, int64_t b, uint32_t alpha32,
+                           const float (&row0)[32], const float (&row1)[32], Slot* slot, int* ambiguous) {
+  Header* h = L.h;
+  const int tid = threadIdx.x, lane = tid & 63;
+  if (tid < 64) {
+    const int n = (int)(b - a);
+    const int V = r.V, blank = r.blank, S = r.S, U = r.U;
+    auto argmax = [&](const float (&row)[32], int f, int& g, float& fs) -> bool {
+      g = -2;
+      fs = 0.0f;
+      if (f >= n) return false;
+      float best = NEG_INF;
+      int chosen = -1;
+      bool dup = false;
+#pragma unroll
+      for (int c = 0; c < 32; ++c) {
+        if (c < V) {
+          // columns outside the alphabet read as -inf: they cannot win and only
+          // tie a -inf maximum, which rejects the chunk anyway
+          const float v = (alpha32 >> c) & 1u ? row[c] : NEG_INF;
+          const bool gt = v > best, eq = v == best;
+          best = gt ? v : best;
+          chosen = gt ? c : chosen;
+          dup = gt ? false : (dup || eq);
+        }
+      }
+      g = chosen;
+      fs = best;
+      return !isfinite(best) || dup;
+    };
+    int g0, g1;
+    float fs0, fs1;
+    const bool bad0 = argmax(row0, lane, g0, fs0);
+    const bool bad1 = argmax(row1, lane + 64, g1, fs1);
+    int accepted = 0, amb = 0;
+    if (__ballot(bad0 || bad1) == 0) {
+      // relative walk (cu:112-117) and token change points, packed r | count << 16
+      const int gp0 = wave_shr1_int(g0, -1);
+      const int gp1 = wave_shr1_int(g1, __builtin_amdgcn_readlane(g0, 63));
+      auto step = [&](int f, int g, int gp, int& inc, int& tc) {
+        inc = tc = 0;
+        if (f >= n) return;
+        if (f > 0) inc = g == gp ? 0 : (g == blank || gp == blank ? 1 : 2);
+        tc = g != blank && (f == 0 || g != gp);
+      };
+      int inc0, tc0, inc1, tc1;
+      step(lane, g0, gp0, inc0, tc0);
+      step(lane + 64, g1, gp1, inc1, tc1);
+      const int v0 = wave_scan_dpp(inc0 | (tc0 << 16));
+      const int v1 = wave_scan_dpp(inc1 | (tc1 << 16)) + __builtin_amdgcn_readlane(v0, 63);
+      const int m = __builtin_amdgcn_readlane(v1, 63) >> 16;
+      const int rlast = (n <= 64 ? __builtin_amdgcn_readlane(v0, n - 1) : __builtin_amdgcn_readlane(v1, n - 65)) & 0xffff;
+      if (tc0) { L.pc[(v0 >> 16) - 1] = g0; L.pd[(v0 >> 16) - 1] = v0 & 0xffff; }
+      if (tc1) { L.pc[(v1 >> 16) - 1] = g1; L.pd[(v1 >> 16) - 1] = v1 & 0xffff; }
+      const bool at_start = a == 0, at_end = b == r.T;
+      int matches = 0, start = -1;
+      if (m == 0) {  // all-blank chunk: closed form of the placement loop (cu:119-134)
+        if (at_start && at_end) { matches = (S == 1) ? 1 : 0; start = 0; }
+        else if (at_start) { matches = 1; start = 0; }
+        else if (at_end) { matches = 1; start = S - 1; }
+        else { matches = (S + 1) / 2; start = 0; }
+      } else {
+        const int r1 = L.pd[0];
+        const int pre = min(m, 3);
+        const int c1 = L.pc[0], c2 = pre > 1 ? L.pc[1] : 0, c3 = pre > 2 ? L.pc[2] : 0;
+        auto placeable = [&](int j) {  // cu:119-123 for target position j (state 2j+1-r1)
+          const int s = 2 * j + 1 - r1;
+          const int terminal = s + rlast;
+          return !((at_start && s > 1) || terminal >= S || (at_end && terminal < S - 2));
+        };
+        int count = 0;
+        for (int base = 0; base + m <= U; base += 64) {  // prefilter on three tokens, ballot compaction
+          const int j = base + lane;
+          bool hit = j + m <= U && L.ytok[j] == c1;
+          if (hit && pre > 1) hit = L.ytok[j + 1] == c2;
+          if (hit && pre > 2) hit = L.ytok[j + 2] == c3;
+          hit = hit && placeable(j);
+          const uint64_t mask = __ballot(hit);
+          if (hit) {
+            const int k = count + (int)lanes_below(mask);
+            if (k < CAND_CAP) { L.cand[k] = j; L.candok[k] = 1; }
+          }
+          count += __popcll(mask);
+        }
+        if (count <= CAND_CAP) {
+          const int width = m - pre;
+          for (int q = lane; q < count * width; q += 64) {
+            const int ci = q / width, i = pre + q % width;
+            if (L.ytok[L.cand[ci] + i] != L.pc[i]) L.candok[ci] = 0;
+          }
+          for (int base = 0; base < count; base += 64) {
+            const int ci = base + lane;
+            const bool ok = ci < count && L.candok[ci];
+            const uint64_t mask = __ballot(ok);
+            if (mask && start < 0)
+              start = 2 * __builtin_amdgcn_readlane(ci < count ? L.cand[ci] : 0, __builtin_ctzll(mask)) + 1 - r1;
+            matches += __popcll(mask);
+          }
+        } else {
+          // more prefiltered candidates than the list holds: exact scan
+          for (int j = lane; j + m <= U; j += 64) {
+            bool hit = placeable(j);
+            for (int i = 0; i < m && hit; ++i) hit = L.ytok[j + i] == L.pc[i];
+            const uint64_t mask = __ballot(hit);
+            if (mask && start < 0) start = 2 * __builtin_amdgcn_readlane(j, __builtin_ctzll(mask)) + 1 - r1;
+            matches += __popcll(mask);
+          }
+        }
+      }
+      amb = matches > 1;
+      if (matches == 1) {
+        // serial fp32 chunk objective in frame order (cu:135-137)
+        float score = readlane_f(fs0, 0);
+        for (int i = 1; i < min(n, 64); ++i) score += readlane_f(fs0, i);
+        for (int i = 0; i < n - 64; ++i) score += readlane_f(fs1, i);
+        if (isfinite(score)) {  // cu:139
+          accepted = 1;
+          if (lane < n) { r.labels[a + lane] = g0; r.scores[a + lane] = fs0; }
+          if (lane + 64 < n) { r.labels[a + lane + 64] = g1; r.scores[a + lane + 64] = fs1; }
+          if (lane == 0) {
+            slot->start = start;
+            slot->end = start + rlast;
+            slot->objective = score;
+          }
+        }
+      }
+    }
+    if (lane == 0) { h->ibuf[3] = accepted; h->ibuf[4] = amb; }
+  }
+  __syncthreads();
+  const int accepted = h->ibuf[3];
+  *ambiguous = h->ibuf[4];
+  __syncthreads();
+  return accepted;
 }
 
 // ---------------------------------------------------------------------------
 // Kernels.
-
-// One workgroup per record: statuses and diagnostics (pack_inputs, cu:819-877).
-__global__ void __launch_bounds__(256) pack_kernel(Params p) {
-  __shared__ Header hh;
-  const int rec = blockIdx.x;
-  const RecordDesc d = p.desc[rec];
-  const int status = record_status(d, p, rec, &hh);
-  if (threadIdx.x == 0) {
-    p.status[rec] = status;
-    p.objective[rec] = NEG_INF;
-    p.stitched[rec] = 0;
-    p.repair_passes[rec] = 0;
-    p.repaired_frames[rec] = 0;
-    for (int q = 0; q < 3; ++q) { p.shortcut_stats[3 * rec + q] = 0; p.routing_stats[3 * rec + q] = 0; }
-    if (p.reuse_stats)
-      for (int q = 0; q < 4; ++q) p.reuse_stats[4 * rec + q] = 0;
-    if (p.arrivals) p.arrivals[rec] = 0;
-  }
-  if (p.mode != 0) {
-    const int64_t T = d.frames;
-    const int n = (int)(1 + (T - 1) / p.H);
-    for (int c = threadIdx.x; c < n; c += blockDim.x) {  // cu:844-851
-      Slot s;
-      s.a = (int)min((int64_t)c * p.H, T);
-      s.b = (int)min((int64_t)(c + 1) * p.H, T);
-      s.flag = 1;
-      s.start = 0;
-      s.end = 0;
-      s.shortcut = 0;
-      s.frontier_end = 0;
-      s.objective = NEG_INF;
-      p.slots[d.chunk_offset + c] = s;
-    }
-  }
-}
 
 template <int K, int D>
 __global__ void __launch_bounds__(K == 32 ? 640 : 256) conventional_kernel(Params p) {
@@ -727,48 +951,200 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) conventional_kernel(Param
   const int rec = blockIdx.x;
   const RecordDesc d = p.desc[rec];
   Rec r = make_rec(d, p, L);
-  const int status = record_status(d, p, rec, L.h);
+  const Staged st = stage_tokens(d, p, rec, L, ALPHABET_NONE);
   if (threadIdx.x == 0) {
     p.stitched[rec] = 0;
     p.repair_passes[rec] = 0;
     p.repaired_frames[rec] = 0;
     for (int q = 0; q < 3; ++q) { p.shortcut_stats[3 * rec + q] = 0; p.routing_stats[3 * rec + q] = 0; }
   }
-  if (status >= 2) {
-    if (threadIdx.x == 0) { p.status[rec] = status; p.objective[rec] = NEG_INF; }
+  if (st.status >= 2) {
+    if (threadIdx.x == 0) { p.status[rec] = st.status; p.objective[rec] = NEG_INF; }
     write_failed(r, 0, r.T);
     return;
   }
-  load_tokens(r, L.ytok);
   const DPOut o = dp_interval<K, D>(r, L, 0, r.T, true, nullptr, 1, nullptr, TRACE_IF_FINITE);
   const bool ok = isfinite(o.score);
   if (threadIdx.x == 0) { p.status[rec] = ok ? 0 : 1; p.objective[rec] = o.score; }  // cu:507-510
   if (!ok) write_failed(r, 0, r.T);
 }
 
-// The record tail of optimized mode, run by the last chunk workgroup of a
-// record to finish: repair rounds, seam validation, fallback and final path.
+// XCD-aware placement: workgroup i runs on XCD i % 8, so consecutive slots of
+// one record (which share its targets) are mapped to the same XCD's L2.
+__device__ inline int xcd_slot(int bid, int total) {
+  const int per = (total + 7) / 8;
+  return (bid % 8) * per + bid / 8;
+}
+
+// Optimized mode, one workgroup per 128-frame chunk: greedy shortcut, else
+// relaxed chunk DP (cu:721-726). Writes the chunk's labels/scores and its slot.
 template <int K, int D>
-__device__ void record_tail(const Params& p, const RecordDesc& d, int rec, const Rec& r, const Lds& L) {
+__global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  const Lds L = carve(lds_raw, p);
+  const int slot_index = xcd_slot(blockIdx.x, p.total_slots);
+  if (slot_index >= p.total_slots) return;
+  const int rec = p.slot_record[slot_index];
+  const RecordDesc d = p.desc[rec];
+  const Rec r = make_rec(d, p, L);
+  const int chunk = slot_index - d.chunk_offset;
+  const int64_t a = (int64_t)chunk * p.H;
+  const int64_t b = min(r.T, a + p.H);
+  const int n = (int)(b - a);
+  const int tid = threadIdx.x;
+  // Issue the chunk's emission rows first so their latency overlaps target
+  // staging: for V <= 32, lane l of wave 0 loads rows a+l and a+64+l.
+  const bool fast = p.mode == 2 && d.vocab <= 32 && (d.vocab & 3) == 0 &&
+                    (reinterpret_cast<uintptr_t>(d.emissions) & 15) == 0 && n <= 128;
+  float row0[32], row1[32];
+#pragma unroll
+  for (int c = 0; c < 32; ++c) { row0[c] = NEG_INF; row1[c] = NEG_INF; }
+  if (fast && tid < 64) {
+    auto load_row = [&](int f, float (&row)[32]) {
+      const float4* src = reinterpret_cast<const float4*>(d.emissions + (a + f) * (int64_t)d.vocab);
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (4 * q < d.vocab) {
+          const float4 v = src[q];
+          row[4 * q] = v.x; row[4 * q + 1] = v.y; row[4 * q + 2] = v.z; row[4 * q + 3] = v.w;
+        }
+    };
+    if (tid < n) load_row(tid, row0);
+    if (tid + 64 < n) load_row(tid + 64, row1);
+  }
+  const Staged st = stage_tokens(d, p, rec, L, p.mode != 2 ? ALPHABET_NONE : (fast ? ALPHABET_MASK32 : ALPHABET_BITMAP));
+  Slot* slot = p.slots + slot_index;
+  if (st.status >= 2) {  // rejected before any label-indexed read (cu:36, cu:642-652)
+    write_failed(r, a, b);
+    if (tid == 0) {
+      Slot s{};
+      s.a = (int)a; s.b = (int)b; s.objective = NEG_INF; s.status = (int16_t)st.status;
+      *slot = s;
+    }
+    return;
+  }
+  int accepted = 0, ambiguous = 0;
+  if (p.mode == 2)
+    accepted = fast ? greedy_wave(r, L, a, b, st.alpha32, row0, row1, slot, &ambiguous)
+                    : greedy_chunk(r, L, a, b, slot, &ambiguous);
+  if (!accepted) {  // initial chunk DP (cu:721-726), relaxed init for a > 0
+    float* fr = r.frontier ? r.frontier + (int64_t)chunk * r.S : nullptr;
+    const DPOut o = dp_interval<K, D>(r, L, a, b, b == r.T, nullptr, a + 1, fr, TRACE_ALWAYS);
+    if (tid == 0) {
+      slot->objective = o.score;
+      slot->end = o.terminal;
+      slot->start = o.start;
+    }
+  }
+  if (tid == 0) {
+    slot->a = (int)a;
+    slot->b = (int)b;
+    slot->flag = 1;
+    slot->kind = (int16_t)(accepted ? 1 : (ambiguous ? 2 : 0));
+    slot->status = 0;
+    slot->frontier_end = (!accepted && r.frontier) ? (int)b : 0;
+  }
+}
+
+// Optimized mode, one workgroup per record, after the chunk kernel: repair
+// rounds, seam validation, full-DP fallback, final path and every per-record
+// output (plan_repairs cu:164-228, repair DP cu:727-760, validate_seams
+// cu:562-592, fallback_recurrence cu:552-559, finish cu:642-667).
+template <int K, int D>
+__global__ void __launch_bounds__(K == 32 ? 640 : 256) tail_kernel(Params p) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  const Lds L = carve(lds_raw, p);
   Header* h = L.h;
+  const int rec = blockIdx.x;
+  const RecordDesc d = p.desc[rec];
+  const Rec r = make_rec(d, p, L);
   const int tid = threadIdx.x;
   const int64_t T = r.T;
   const int n = (int)(1 + (T - 1) / p.H);
   Slot* gs = p.slots + d.chunk_offset;
   Slot* sl = gs;
-  const bool in_lds = n <= p.lds_tail_slots;
-  if (in_lds) {
+  if (n <= p.lds_tail_slots) {
     for (int c = tid; c < n; c += blockDim.x) L.tslots[c] = gs[c];
     __syncthreads();
     sl = L.tslots;
   }
+  const int status0 = sl[0].status;
+  if (status0 >= 2) {
+    if (tid == 0) {
+      p.status[rec] = status0;
+      p.objective[rec] = NEG_INF;
+      p.stitched[rec] = 0;
+      p.repair_passes[rec] = 0;
+      p.repaired_frames[rec] = 0;
+      for (int q = 0; q < 3; ++q) { p.shortcut_stats[3 * rec + q] = 0; p.routing_stats[3 * rec + q] = 0; }
+      if (p.reuse_stats)
+        for (int q = 0; q < 4; ++q) p.reuse_stats[4 * rec + q] = 0;
+    }
+    return;
+  }
+  load_tokens(r, L.ytok);
   const int S = r.S;
   const bool frontier_on = r.frontier != nullptr;
+  // Fast path (records of at most 64 chunks, slots in LDS): when every chunk
+  // objective is finite and every seam is legal, the repair rounds merge
+  // nothing (plan_repairs joins every neighbour and its budget preflight
+  // proposes no region) and validate_seams stitches iff the fp32 total is
+  // finite. Wave 0 checks all seams at once and writes the result.
+  if (n <= 64 && sl == L.tslots) {
+    if (tid < 64) {
+      const int k = tid;
+      const bool valid = k < n;
+      const Slot sk = sl[valid ? k : 0];
+      const int end_prev = (valid && k > 0) ? sl[k - 1].end : 0;
+      const bool ok = !valid || (isfinite(sk.objective) && (k == 0 || legal_seam(r, sk.start, end_prev)));
+      int done = 0;
+      if (__ballot(!ok) == 0) {
+        float total = 0.0f;  // cu:578-584: chunk objectives summed in chunk order
+        for (int i = 0; i < n; ++i) total += readlane_f(sk.objective, i);
+        if (isfinite(total)) {
+          done = 1;
+          const uint64_t shortcut = __ballot(valid && sk.kind == 1);
+          const uint64_t amb = __ballot(valid && sk.kind == 2);
+          const uint64_t dp = __ballot(valid && sk.kind != 1);
+          int frames = valid && sk.kind == 1 ? sk.b - sk.a : 0;
+#pragma unroll
+          for (int off = 32; off > 0; off >>= 1) frames += __shfl_xor(frames, off, 64);
+          if (tid == 0) {
+            p.status[rec] = 0;
+            p.objective[rec] = total;
+            p.stitched[rec] = 1;
+            p.repair_passes[rec] = 0;
+            p.repaired_frames[rec] = 0;
+            p.shortcut_stats[3 * rec + 0] = __popcll(shortcut);
+            p.shortcut_stats[3 * rec + 1] = frames;
+            p.shortcut_stats[3 * rec + 2] = __popcll(amb);
+            for (int q = 0; q < 3; ++q) p.routing_stats[3 * rec + q] = 0;
+            if (p.reuse_stats) {
+              int64_t* u = p.reuse_stats + 4 * rec;
+              u[0] = 0; u[1] = 0; u[2] = frontier_on ? (int64_t)__popcll(dp) * S : 0; u[3] = 0;
+            }
+          }
+        }
+      }
+      if (tid == 0) h->ibuf[6] = done;
+    }
+    __syncthreads();
+    if (h->ibuf[6]) return;
+    __syncthreads();
+  }
+  int64_t sc_accepted = 0, sc_frames = 0, sc_ambiguous = 0;
   int64_t reuse0 = 0, reuse1 = 0, reuse2 = 0, reuse3 = 0;
+  if (tid == 0) {  // shortcut_stats (cu:129-133, 140-146) and frontier writes of the chunk DPs
+    for (int k = 0; k < n; ++k) {
+      if (sl[k].kind == 1) { ++sc_accepted; sc_frames += sl[k].b - sl[k].a; }
+      else {
+        if (sl[k].kind == 2) ++sc_ambiguous;
+        if (frontier_on) reuse2 += S;
+      }
+    }
+  }
   int early = 0, rejected = 0, maxprop = 0, passes = 0;
   int64_t repaired = 0;
-  int term = 0;
-  float fscore = NEG_INF;
   int status = 0;
   float objective = NEG_INF;
   const bool repairs = p.repair_rounds > 0;
@@ -833,8 +1209,6 @@ __device__ void record_tail(const Params& p, const RecordDesc& d, int rec, const
         if (resume) { reuse1 += s0.frontier_end; reuse3 += S; }
         const DPOut o = dp_interval<K, D>(r, L, 0, T, true, resume ? r.frontier : nullptr,
                                           resume ? s0.frontier_end : 1, nullptr, TRACE_IF_FINITE);
-        term = o.terminal;
-        fscore = o.score;
         status = isfinite(o.score) ? 0 : 1;
         objective = o.score;
         early = 2;
@@ -899,14 +1273,10 @@ __device__ void record_tail(const Params& p, const RecordDesc& d, int rec, const
       if (resume) { reuse1 += s0.frontier_end; reuse3 += S; }
       const DPOut o = dp_interval<K, D>(r, L, 0, T, true, resume ? r.frontier : nullptr,
                                         resume ? s0.frontier_end : 1, nullptr, TRACE_IF_FINITE);
-      term = o.terminal;
-      fscore = o.score;
       status = isfinite(o.score) ? 0 : 1;
       objective = o.score;
     }
   }
-  (void)term;
-  (void)fscore;
   if (status != 0) write_failed(r, 0, T);
   if (tid == 0) {
     p.status[rec] = status;
@@ -914,72 +1284,17 @@ __device__ void record_tail(const Params& p, const RecordDesc& d, int rec, const
     p.stitched[rec] = stitched;
     p.repair_passes[rec] = passes;
     p.repaired_frames[rec] = repaired;
+    p.shortcut_stats[3 * rec + 0] = sc_accepted;
+    p.shortcut_stats[3 * rec + 1] = sc_frames;
+    p.shortcut_stats[3 * rec + 2] = sc_ambiguous;
     p.routing_stats[3 * rec + 0] = early;
     p.routing_stats[3 * rec + 1] = rejected;
     p.routing_stats[3 * rec + 2] = maxprop;
-    if (p.reuse_stats && r.frontier) {
-      atomicAdd(reinterpret_cast<unsigned long long*>(&p.reuse_stats[4 * rec + 0]), (unsigned long long)reuse0);
-      atomicAdd(reinterpret_cast<unsigned long long*>(&p.reuse_stats[4 * rec + 1]), (unsigned long long)reuse1);
-      atomicAdd(reinterpret_cast<unsigned long long*>(&p.reuse_stats[4 * rec + 2]), (unsigned long long)reuse2);
-      atomicAdd(reinterpret_cast<unsigned long long*>(&p.reuse_stats[4 * rec + 3]), (unsigned long long)reuse3);
+    if (p.reuse_stats) {
+      int64_t* u = p.reuse_stats + 4 * rec;
+      u[0] = reuse0; u[1] = reuse1; u[2] = reuse2; u[3] = reuse3;
     }
   }
-}
-
-template <int K, int D>
-__global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
-  extern __shared__ __align__(16) unsigned char lds_raw[];
-  const Lds L = carve(lds_raw, p);
-  Header* h = L.h;
-  const int slot_index = blockIdx.x;
-  const int rec = p.slot_record[slot_index];
-  const RecordDesc d = p.desc[rec];
-  const Rec r = make_rec(d, p, L);
-  const int chunk = slot_index - d.chunk_offset;
-  const int64_t a = (int64_t)chunk * p.H;
-  const int64_t b = min(r.T, a + p.H);
-  const int status = p.status[rec];
-  if (status >= 2) {  // rejected before any label-indexed read (cu:36, cu:642-652)
-    write_failed(r, a, b);
-    return;
-  }
-  Slot* slot = p.slots + slot_index;
-  load_tokens(r, L.ytok);
-  int accepted = 0, ambiguous = 0;
-  if (p.mode == 2) accepted = greedy_chunk(r, L, a, b, slot, &ambiguous);
-  if (threadIdx.x == 0) {
-    if (accepted) {
-      atomicAdd(reinterpret_cast<unsigned long long*>(&p.shortcut_stats[3 * rec + 0]), 1ull);
-      atomicAdd(reinterpret_cast<unsigned long long*>(&p.shortcut_stats[3 * rec + 1]), (unsigned long long)(b - a));
-    } else if (ambiguous) {
-      atomicAdd(reinterpret_cast<unsigned long long*>(&p.shortcut_stats[3 * rec + 2]), 1ull);
-    }
-  }
-  if (!accepted) {  // initial chunk DP (cu:721-726), relaxed init for a > 0
-    float* fr = r.frontier ? r.frontier + (int64_t)chunk * r.S : nullptr;
-    const DPOut o = dp_interval<K, D>(r, L, a, b, b == r.T, nullptr, a + 1, fr, TRACE_ALWAYS);
-    if (threadIdx.x == 0) {
-      slot->objective = o.score;
-      slot->end = o.terminal;
-      slot->start = o.start;
-      if (fr) {
-        slot->frontier_end = (int)b;
-        atomicAdd(reinterpret_cast<unsigned long long*>(&p.reuse_stats[4 * rec + 2]), (unsigned long long)r.S);
-      }
-    }
-  }
-  // arrival: the last chunk of the record runs its tail
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __threadfence();
-    const int n = (int)(1 + (r.T - 1) / p.H);
-    const int old = atomicAdd(&p.arrivals[rec], 1);
-    h->ibuf[7] = old == n - 1;
-  }
-  __syncthreads();
-  if (!h->ibuf[7]) return;
-  __threadfence();
-  record_tail<K, D>(p, d, rec, r, L);
 }
 
 // One workgroup per record: any NaN or +inf rejects it (cu:881-891).
@@ -1029,21 +1344,22 @@ inline int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 // internal[] of ffa_align_plan
 enum {
   I_K, I_NT, I_SLOTS, I_LDS, I_UCAP, I_DCAP, I_VWORDS, I_TAILSLOTS, I_FRONTIER, I_BUDGET,
-  I_OVERLAP, I_WS_SLOTS, I_WS_ARRIVALS, I_WS_FRONTIER, I_MODE, I_H, I_FMIN, I_REPAIR_MIN
+  I_OVERLAP, I_WS_SLOTS, I_WS_FRONTIER, I_MODE, I_H, I_FMIN, I_REPAIR_MIN
 };
 
 template <int K, int D>
 int launch_geometry(const ffa::Params& p, int NT, size_t lds, bool optimized, hipStream_t stream) {
   hipEvent_t start = g_profile_start, stop = g_profile_stop;
   g_profile_start = g_profile_stop = nullptr;
-  if (optimized) hipLaunchKernelGGL(ffa::pack_kernel, dim3(p.count), dim3(256), 0, stream, p);
   if (start) hipEventRecord(start, stream);
   if (!optimized) {
     hipLaunchKernelGGL((ffa::conventional_kernel<K, D>), dim3(p.count), dim3(NT), lds, stream, p);
   } else {
-    hipLaunchKernelGGL((ffa::chunk_kernel<K, D>), dim3(p.total_slots), dim3(NT), lds, stream, p);
+    const int grid = 8 * ((p.total_slots + 7) / 8);
+    hipLaunchKernelGGL((ffa::chunk_kernel<K, D>), dim3(grid), dim3(std::max(NT, 128)), lds, stream, p);
   }
   if (stop) hipEventRecord(stop, stream);
+  if (optimized) hipLaunchKernelGGL((ffa::tail_kernel<K, D>), dim3(p.count), dim3(NT), lds, stream, p);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(FFA_E_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
   return FFA_OK;
@@ -1157,15 +1473,13 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
   geometry(s_max, &K, &NT);
   const int64_t v_words = (v_max + 31) / 32;
   const int64_t tail_slots = optimized ? std::min<int64_t>(n_max, ffa::TAIL_SLOT_CAP) : 0;
-  const int64_t greedy_bytes = optimized ? 20 * H + align_up(2 * d_cap, 16) + 8 * v_words : 0;
+  const int64_t greedy_bytes = 20 * align_up(H, 32) + 2048 + align_up(2 * d_cap, 16) + 8 * v_words;
   const int64_t region = std::max(greedy_bytes, 32 * tail_slots);
   const int64_t lds = align_up((int64_t)sizeof(ffa::Header), 16) + align_up(2 * std::max<int64_t>(u_max, 1), 16) + region;
   if (lds > 64 * 1024) return fail(FFA_E_INVALID, "batch needs more than 64 KiB of LDS per workgroup");
   int64_t ws = align_up(4 * bp_words, 256);
   const int64_t ws_slots = ws;
   ws += align_up(32 * slots, 256);
-  const int64_t ws_arrivals = ws;
-  ws += optimized ? align_up(4 * count, 256) : 0;
   const int64_t ws_frontier = ws;
   ws += align_up(4 * frontier_floats, 256);
   std::memset(plan, 0, sizeof(*plan));
@@ -1187,7 +1501,6 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
   in[I_BUDGET] = budget_on ? o->repair_budget_frames : 0;
   in[I_OVERLAP] = (budget_on && o->overlap_fallback) ? 1 : 0;
   in[I_WS_SLOTS] = ws_slots;
-  in[I_WS_ARRIVALS] = ws_arrivals;
   in[I_WS_FRONTIER] = ws_frontier;
   in[I_MODE] = o->mode;
   in[I_H] = H;
@@ -1266,7 +1579,6 @@ extern "C" int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_opti
   auto* ws = static_cast<unsigned char*>(workspace);
   p.bp = reinterpret_cast<uint32_t*>(ws);
   p.slots = reinterpret_cast<ffa::Slot*>(ws + in[I_WS_SLOTS]);
-  p.arrivals = optimized ? reinterpret_cast<int32_t*>(ws + in[I_WS_ARRIVALS]) : nullptr;
   p.frontiers = reinterpret_cast<float*>(ws + in[I_WS_FRONTIER]);
   p.budget = in[I_BUDGET];
   p.repair_min = in[I_REPAIR_MIN];
