@@ -43,6 +43,7 @@ namespace ffa {
 constexpr float NEG_INF = -INFINITY;
 constexpr int MAX_H = 512;          // chunk_frames supported by the LDS layout
 constexpr int TAIL_SLOT_CAP = 512;  // record tails with more chunks plan in global memory
+constexpr int YTOK_PAD = 72;        // sentinel entries after the staged targets
 
 struct RecordDesc {  // device descriptor table entry, 64 bytes
   const float* emissions;
@@ -65,9 +66,15 @@ struct Slot {  // per-chunk state of optimized mode (cu:1021-1029 buffers), 32 b
 };
 static_assert(sizeof(Slot) == 32, "slot layout");
 
+struct SlotEntry {  // per-chunk table entry: the chunk's first emission row and owner
+  const float* rows;
+  int32_t record, chunk;
+};
+static_assert(sizeof(SlotEntry) == 16, "slot entry layout");
+
 struct Params {
   const RecordDesc* desc;
-  const int32_t* slot_record;
+  const SlotEntry* slot_entries;
   const uint8_t* validity;
   int64_t* labels;
   float* scores;
@@ -126,7 +133,7 @@ __device__ inline Lds carve(unsigned char* base, const Params& p) {
   L.h = reinterpret_cast<Header*>(base);
   off = align16(sizeof(Header));
   L.ytok = reinterpret_cast<int16_t*>(base + off);
-  off = align16(off + 2 * (size_t)p.u_cap);
+  off = align16(off + 2 * ((size_t)p.u_cap + YTOK_PAD));
   unsigned char* region = base + off;
   size_t g = 0;
   const size_t h32 = (size_t)((p.H + 31) & ~31);
@@ -144,11 +151,38 @@ __device__ inline Lds carve(unsigned char* base, const Params& p) {
   return L;
 }
 
-// Loads through the global address space: the pointers come from the
-// descriptor table, so the compiler cannot infer it and would emit flat loads.
-typedef const __attribute__((address_space(1))) char gchar_t;
-__device__ inline float ldg_at(const void* base, uint32_t byte_offset) {
-  return *(const __attribute__((address_space(1))) float*)((gchar_t*)base + byte_offset);
+// Pointers read from the descriptor table or the parameter block are generic
+// to the compiler, which would emit flat accesses; flat loads also count
+// against lgkmcnt, so every LDS wait would stall on outstanding HBM reads.
+// Device code therefore accesses global memory through address space 1.
+#define GLB __attribute__((address_space(1)))
+template <class T>
+__device__ inline GLB T* glb(T* x) { return (GLB T*)x; }
+template <class T>
+__device__ inline const GLB T* glb(const T* x) { return (const GLB T*)x; }
+__device__ inline float ldg_at(const GLB float* base, uint32_t byte_offset) {
+  return *(const GLB float*)((const GLB char*)base + byte_offset);
+}
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+typedef float v4f_t __attribute__((ext_vector_type(4)));
+// Whole-struct copies to and from global memory (16-byte vector moves).
+template <class T>
+__device__ inline T load_pod(const GLB T* src) {
+  static_assert(sizeof(T) % 16 == 0, "16-byte granules");
+  v4i_t tmp[sizeof(T) / 16];
+#pragma unroll
+  for (size_t i = 0; i < sizeof(T) / 16; ++i) tmp[i] = ((const GLB v4i_t*)src)[i];
+  T out;
+  __builtin_memcpy(&out, tmp, sizeof(T));
+  return out;
+}
+template <class T>
+__device__ inline void store_pod(GLB T* dst, const T& value) {
+  static_assert(sizeof(T) % 16 == 0, "16-byte granules");
+  v4i_t tmp[sizeof(T) / 16];
+  __builtin_memcpy(tmp, &value, sizeof(T));
+#pragma unroll
+  for (size_t i = 0; i < sizeof(T) / 16; ++i) ((GLB v4i_t*)dst)[i] = tmp[i];
 }
 
 // ---------------------------------------------------------------------------
@@ -271,32 +305,32 @@ __device__ inline int block_min(int x, Header* h) {
 // ---------------------------------------------------------------------------
 // Record view shared by all device routines.
 struct Rec {
-  const float* e;
-  const int64_t* y;
+  const GLB float* e;
+  const GLB int64_t* y;
   int64_t T;
   int32_t V, U, S, blank;
   int32_t stride;  // backpointer row, words
-  uint32_t* bp;
-  float* frontier;  // this record's frontier block, or nullptr
-  int64_t* labels;  // this record's output rows
-  float* scores;
+  GLB uint32_t* bp;
+  GLB float* frontier;  // this record's frontier block, or nullptr
+  GLB int64_t* labels;  // this record's output rows
+  GLB float* scores;
   const int16_t* ytok;
 };
 
 __device__ inline Rec make_rec(const RecordDesc& d, const Params& p, const Lds& L) {
   Rec r;
-  r.e = d.emissions;
-  r.y = d.targets;
+  r.e = glb(d.emissions);
+  r.y = glb(d.targets);
   r.T = d.frames;
   r.V = d.vocab;
   r.U = d.tokens;
   r.S = 2 * d.tokens + 1;
   r.blank = d.blank;
   r.stride = 2 * ((r.S + 31) / 32);
-  r.bp = p.bp + d.bp_offset;
-  r.frontier = d.frontier_offset >= 0 ? p.frontiers + d.frontier_offset : nullptr;
-  r.labels = p.labels + d.frame_offset;
-  r.scores = p.scores + d.frame_offset;
+  r.bp = glb(p.bp) + d.bp_offset;
+  r.frontier = d.frontier_offset >= 0 ? glb(p.frontiers) + d.frontier_offset : nullptr;
+  r.labels = glb(p.labels) + d.frame_offset;
+  r.scores = glb(p.scores) + d.frame_offset;
   r.ytok = L.ytok;
   return r;
 }
@@ -323,9 +357,9 @@ struct DPOut {
 enum { TRACE_NONE = 0, TRACE_ALWAYS = 1, TRACE_IF_FINITE = 2 };
 
 template <int K>
-__device__ inline void store_bits(uint32_t* row, int tid, uint32_t bits) {
-  if constexpr (K == 4) reinterpret_cast<uint8_t*>(row)[tid] = (uint8_t)bits;
-  else if constexpr (K == 8) reinterpret_cast<uint16_t*>(row)[tid] = (uint16_t)bits;
+__device__ inline void store_bits(GLB uint32_t* row, int tid, uint32_t bits) {
+  if constexpr (K == 4) ((GLB uint8_t*)row)[tid] = (uint8_t)bits;
+  else if constexpr (K == 8) ((GLB uint16_t*)row)[tid] = (uint16_t)bits;
   else if constexpr (K == 16) row[tid] = bits;
   else { row[2 * tid] = bits; }
 }
@@ -336,7 +370,7 @@ template <>
 struct BitsT<32> { using type = uint64_t; };
 
 template <int K>
-__device__ inline void store_row(uint32_t* row, int tid, typename BitsT<K>::type bits) {
+__device__ inline void store_row(GLB uint32_t* row, int tid, typename BitsT<K>::type bits) {
   if constexpr (K == 32) {
     row[2 * tid] = (uint32_t)bits;
     row[2 * tid + 1] = (uint32_t)(bits >> 32);
@@ -359,7 +393,7 @@ __device__ inline int trace_path(const Rec& r, int64_t a, int64_t b, int termina
     uint32_t vhi = 0, vlo = 0;
     const int64_t ti = t - lane;
     if (ti >= a) {
-      const uint32_t* row = r.bp + ti * (int64_t)r.stride;
+      const GLB uint32_t* row = r.bp + ti * (int64_t)r.stride;
       vhi = row[whi];
       if (whi > 0) vlo = row[whi - 1];
     }
@@ -390,8 +424,8 @@ __device__ inline int trace_path(const Rec& r, int64_t a, int64_t b, int termina
 }
 
 template <int K, int D>
-__device__ DPOut dp_interval(const Rec& r, const Lds& L, int64_t a, int64_t b, bool record_end,
-                             const float* resume_from, int64_t start_t, float* save_frontier, int trace) {
+__device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const Lds& L, int64_t a, int64_t b, bool record_end,
+                             const GLB float* resume_from, int64_t start_t, GLB float* save_frontier, int trace) {
   using Bits = typename BitsT<K>::type;
   Header* h = L.h;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
@@ -412,14 +446,14 @@ __device__ DPOut dp_interval(const Rec& r, const Lds& L, int64_t a, int64_t b, b
     if constexpr (kMask) skm |= (uint32_t)ok << k;
     else skb[k] = ok ? 0.0f : NEG_INF;
   }
-  const float* e = r.e;
+  const GLB float* e = r.e;
   const int64_t V = r.V;
-  uint32_t* bp = r.bp;
+  GLB uint32_t* bp = r.bp;
   if (resume_from) {
 #pragma unroll
     for (int k = 0; k < K; ++k) al[k] = (s0 + k < S) ? resume_from[s0 + k] : NEG_INF;
   } else {
-    const float* row = e + a * V;
+    const GLB float* row = e + a * V;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       const float v = ldg_at(row, lab[k]);
@@ -477,7 +511,7 @@ __device__ DPOut dp_interval(const Rec& r, const Lds& L, int64_t a, int64_t b, b
   float ev[D][K];
 #pragma unroll
   for (int d = 0; d < D; ++d) {
-    const float* row = e + min(start_t + d, last) * V;
+    const GLB float* row = e + min(start_t + d, last) * V;
 #pragma unroll
     for (int k = 0; k < K; ++k) ev[d][k] = ldg_at(row, lab[k]);
   }
@@ -486,7 +520,7 @@ __device__ DPOut dp_interval(const Rec& r, const Lds& L, int64_t a, int64_t b, b
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       frame(t0 + d, ev[d]);
-      const float* row = e + min(t0 + d + D, last) * V;
+      const GLB float* row = e + min(t0 + d + D, last) * V;
 #pragma unroll
       for (int k = 0; k < K; ++k) ev[d][k] = ldg_at(row, lab[k]);
     }
@@ -571,18 +605,37 @@ __device__ Staged stage_tokens(const RecordDesc& d, const Params& p, int rec, co
   }
   int oov = 0, invalid = 0, repeats = 0;
   uint32_t mask = 0;
-  for (int j = tid; j < d.tokens; j += blockDim.x) {
-    const int64_t tok = d.targets[j];
-    const bool out = tok < 0 || tok >= V;  // checked as int64 before narrowing (cu:860)
-    oov |= out;
-    invalid |= out || tok == d.blank;
-    repeats += j > 0 && tok == d.targets[j - 1];  // cu:861
-    L.ytok[j] = (int16_t)(out ? 0 : tok);
-    if (!out) {
-      if (alphabet == ALPHABET_BITMAP) atomicOr(&L.bitmap[tok >> 5], 1u << (tok & 31));
-      else if (alphabet == ALPHABET_MASK32) mask |= 1u << tok;
+  // thread t checks targets [t*per, (t+1)*per) and compares its first one with
+  // the target before it: one batch of loads in flight per thread
+  const GLB int64_t* y = glb(d.targets);
+  const int U = d.tokens;
+  const int per = (U + (int)blockDim.x - 1) / (int)blockDim.x;
+  const int j0 = tid * per, j1 = min(U, j0 + per);
+  int64_t before = (j0 > 0 && j0 < U) ? y[j0 - 1] : 0;
+  for (int jb = j0; jb < j1; jb += 8) {
+    int64_t v[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) v[q] = y[min(jb + q, j1 - 1)];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int j = jb + q;
+      if (j < j1) {
+        const int64_t tok = v[q];
+        const bool out = tok < 0 || tok >= V;  // checked as int64 before narrowing (cu:860)
+        oov |= out;
+        invalid |= out || tok == d.blank;
+        repeats += j > 0 && tok == before;  // cu:861
+        before = tok;
+        L.ytok[j] = (int16_t)(out ? 0 : tok);
+        if (!out) {
+          if (alphabet == ALPHABET_BITMAP) atomicOr(&L.bitmap[tok >> 5], 1u << (tok & 31));
+          else if (alphabet == ALPHABET_MASK32) mask |= 1u << tok;
+        }
+      }
     }
   }
+  // sentinel padding after the targets: the placement prefilter reads ahead
+  for (int j = U + tid; j < U + YTOK_PAD; j += blockDim.x) L.ytok[j] = -1;
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {  // one reduction for all four values
     oov |= __shfl_xor(oov, off, 64);
@@ -609,7 +662,7 @@ __device__ Staged stage_tokens(const RecordDesc& d, const Params& p, int rec, co
   if (flags & 1) st.status = 3;
   else if (p.check_inputs && (flags & 2)) st.status = 3;                          // cu:872
   else if (p.check_inputs && (int64_t)d.tokens + reps > d.frames) st.status = 4;  // cu:873
-  else st.status = (p.validity && !p.validity[rec]) ? 2 : 0;                     // cu:836
+  else st.status = (p.validity && !glb(p.validity)[rec]) ? 2 : 0;               // cu:836
   return st;
 }
 
@@ -636,7 +689,7 @@ __device__ inline bool legal_seam(const Rec& r, int start, int before) {  // cu:
 // *ambiguous is set when more than one placement is legal.
 constexpr int CAND_CAP = 256;
 
-__device__ int greedy_chunk(const Rec& r, const Lds& L, int64_t a, int64_t b, Slot* slot, int* ambiguous) {
+__device__ int greedy_chunk(const Rec& r, const Lds& L, int64_t a, int64_t b, GLB Slot* slot, int* ambiguous) {
   Header* h = L.h;
   const int tid = threadIdx.x, NT = blockDim.x;
   const int n = (int)(b - a);
@@ -658,7 +711,7 @@ __device__ int greedy_chunk(const Rec& r, const Lds& L, int64_t a, int64_t b, Sl
     }
     __syncthreads();
     for (int f = tid; f < n; f += NT) {
-      const float* row = r.e + (a + f) * (int64_t)V;
+      const GLB float* row = r.e + (a + f) * (int64_t)V;
       float best = NEG_INF;
       int chosen = -1;
       bool dup = false;
@@ -806,41 +859,62 @@ __device__ int greedy_chunk(const Rec& r, const Lds& L, int64_t a, int64_t b, Sl
 // DPP, candidates are compacted with ballots, and the fp32 chunk objective is
 // a readlane chain in frame order. Other waves only wait for the verdict.
 __device__ int greedy_wave(const Rec& r, const Lds& L, int64_t a, int64_t b, uint32_t alpha32,
-                           const float (&row0)[32], const float (&row1)[32], Slot* slot, int* ambiguous) {
+                           const float (&row0)[32], const float (&row1)[32], GLB Slot* slot, int* ambiguous) {
   Header* h = L.h;
-  const int tid = threadIdx.x, lane = tid & 63;
-  if (tid < 64) {
-    const int n = (int)(b - a);
-    const int V = r.V, blank = r.blank, S = r.S, U = r.U;
-    auto argmax = [&](const float (&row)[32], int f, int& g, float& fs) -> bool {
-      g = -2;
-      fs = 0.0f;
-      if (f >= n) return false;
-      float best = NEG_INF;
-      int chosen = -1;
-      bool dup = false;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = (int)(b - a);
+  const int blank = r.blank, S = r.S, U = r.U;
+  int g0 = -2, g1 = -2;
+  float fs0 = 0.0f, fs1 = 0.0f;
+  // Unique maximum over the alphabet columns (cu:65-91). Columns outside the
+  // alphabet (and past V, which hold -inf) read as -inf: they cannot win
+  // and only tie a -inf maximum, which rejects the chunk anyway. A max tree
+  // (IEEE max ignores NaN, as the reference's strict '>' scan does) then
+  // independent equality tests: unique iff exactly one column equals it.
+  // Branch-free, so the two rows of a lane interleave.
+  auto argmax = [&](const float (&row)[32], int f, int& g, float& fs) -> bool {
+    float v[32];
 #pragma unroll
-      for (int c = 0; c < 32; ++c) {
-        if (c < V) {
-          // columns outside the alphabet read as -inf: they cannot win and only
-          // tie a -inf maximum, which rejects the chunk anyway
-          const float v = (alpha32 >> c) & 1u ? row[c] : NEG_INF;
-          const bool gt = v > best, eq = v == best;
-          best = gt ? v : best;
-          chosen = gt ? c : chosen;
-          dup = gt ? false : (dup || eq);
-        }
-      }
-      g = chosen;
-      fs = best;
-      return !isfinite(best) || dup;
-    };
-    int g0, g1;
-    float fs0, fs1;
+    for (int c = 0; c < 32; ++c) v[c] = (alpha32 >> c) & 1u ? row[c] : NEG_INF;
+    float t[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) t[c] = fmaxf(v[2 * c], v[2 * c + 1]);
+#pragma unroll
+    for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+      for (int c = 0; c < w; ++c) t[c] = fmaxf(t[2 * c], t[2 * c + 1]);
+    const float m = t[0];
+    int count = 0, idx = -1;
+#pragma unroll
+    for (int c = 0; c < 32; ++c) {
+      const bool e = v[c] == m;
+      count += e;
+      idx = e ? c : idx;
+    }
+    const bool live = f < n;
+    g = live ? idx : -2;
+    fs = live ? m : 0.0f;
+    return live && (!isfinite(m) || count != 1);
+  };
+  if (wave == 0) {
     const bool bad0 = argmax(row0, lane, g0, fs0);
     const bool bad1 = argmax(row1, lane + 64, g1, fs1);
-    int accepted = 0, amb = 0;
-    if (__ballot(bad0 || bad1) == 0) {
+    L.fs[lane] = fs0;
+    L.fs[lane + 64] = fs1;
+    if (lane == 0) h->ibuf[5] = __ballot(bad0 || bad1) != 0;
+  }
+  __syncthreads();
+  *ambiguous = 0;
+  if (h->ibuf[5]) {  // a tie or a non-finite maximum: no shortcut
+    __syncthreads();
+    return 0;
+  }
+  if (wave == 1) {
+    // the serial fp32 chunk objective (cu:135-137), overlapped with placement
+    if (lane == 0) h->fbuf[1] = serial_sum(L.fs, n);
+  } else if (wave == 0) {
+    int matches = 0, start = -1, rlast = 0;
+    {
       // relative walk (cu:112-117) and token change points, packed r | count << 16
       const int gp0 = wave_shr1_int(g0, -1);
       const int gp1 = wave_shr1_int(g1, __builtin_amdgcn_readlane(g0, 63));
@@ -856,11 +930,10 @@ __device__ int greedy_wave(const Rec& r, const Lds& L, int64_t a, int64_t b, uin
       const int v0 = wave_scan_dpp(inc0 | (tc0 << 16));
       const int v1 = wave_scan_dpp(inc1 | (tc1 << 16)) + __builtin_amdgcn_readlane(v0, 63);
       const int m = __builtin_amdgcn_readlane(v1, 63) >> 16;
-      const int rlast = (n <= 64 ? __builtin_amdgcn_readlane(v0, n - 1) : __builtin_amdgcn_readlane(v1, n - 65)) & 0xffff;
+      rlast = (n <= 64 ? __builtin_amdgcn_readlane(v0, n - 1) : __builtin_amdgcn_readlane(v1, n - 65)) & 0xffff;
       if (tc0) { L.pc[(v0 >> 16) - 1] = g0; L.pd[(v0 >> 16) - 1] = v0 & 0xffff; }
       if (tc1) { L.pc[(v1 >> 16) - 1] = g1; L.pd[(v1 >> 16) - 1] = v1 & 0xffff; }
       const bool at_start = a == 0, at_end = b == r.T;
-      int matches = 0, start = -1;
       if (m == 0) {  // all-blank chunk: closed form of the placement loop (cu:119-134)
         if (at_start && at_end) { matches = (S == 1) ? 1 : 0; start = 0; }
         else if (at_start) { matches = 1; start = 0; }
@@ -876,18 +949,27 @@ __device__ int greedy_wave(const Rec& r, const Lds& L, int64_t a, int64_t b, uin
           return !((at_start && s > 1) || terminal >= S || (at_end && terminal < S - 2));
         };
         int count = 0;
-        for (int base = 0; base + m <= U; base += 64) {  // prefilter on three tokens, ballot compaction
-          const int j = base + lane;
-          bool hit = j + m <= U && L.ytok[j] == c1;
-          if (hit && pre > 1) hit = L.ytok[j + 1] == c2;
-          if (hit && pre > 2) hit = L.ytok[j + 2] == c3;
-          hit = hit && placeable(j);
-          const uint64_t mask = __ballot(hit);
-          if (hit) {
-            const int k = count + (int)lanes_below(mask);
-            if (k < CAND_CAP) { L.cand[k] = j; L.candok[k] = 1; }
+        for (int base = 0; base + m <= U; base += 256) {  // 4 x 64 positions per round of LDS reads
+          int t0[4], t1[4], t2[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {  // clamped: reads at most ytok[U + 2], in the sentinel padding
+            const int j = min(base + 64 * u + lane, U);
+            t0[u] = L.ytok[j];
+            t1[u] = L.ytok[j + 1];
+            t2[u] = L.ytok[j + 2];
           }
-          count += __popcll(mask);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int j = base + 64 * u + lane;
+            const bool hit = (j + m <= U) & (t0[u] == c1) & ((pre < 2) | (t1[u] == c2)) & ((pre < 3) | (t2[u] == c3)) &
+                             placeable(j);
+            const uint64_t mask = __ballot(hit);
+            if (hit) {
+              const int k = count + (int)lanes_below(mask);
+              if (k < CAND_CAP) { L.cand[k] = j; L.candok[k] = 1; }
+            }
+            count += __popcll(mask);
+          }
         }
         if (count <= CAND_CAP) {
           const int width = m - pre;
@@ -905,8 +987,9 @@ __device__ int greedy_wave(const Rec& r, const Lds& L, int64_t a, int64_t b, uin
           }
         } else {
           // more prefiltered candidates than the list holds: exact scan
-          for (int j = lane; j + m <= U; j += 64) {
-            bool hit = placeable(j);
+          for (int base = 0; base + m <= U; base += 64) {  // uniform trip count for the ballots
+            const int j = base + lane;
+            bool hit = j + m <= U && placeable(j);
             for (int i = 0; i < m && hit; ++i) hit = L.ytok[j + i] == L.pc[i];
             const uint64_t mask = __ballot(hit);
             if (mask && start < 0) start = 2 * __builtin_amdgcn_readlane(j, __builtin_ctzll(mask)) + 1 - r1;
@@ -914,31 +997,27 @@ __device__ int greedy_wave(const Rec& r, const Lds& L, int64_t a, int64_t b, uin
           }
         }
       }
-      amb = matches > 1;
-      if (matches == 1) {
-        // serial fp32 chunk objective in frame order (cu:135-137)
-        float score = readlane_f(fs0, 0);
-        for (int i = 1; i < min(n, 64); ++i) score += readlane_f(fs0, i);
-        for (int i = 0; i < n - 64; ++i) score += readlane_f(fs1, i);
-        if (isfinite(score)) {  // cu:139
-          accepted = 1;
-          if (lane < n) { r.labels[a + lane] = g0; r.scores[a + lane] = fs0; }
-          if (lane + 64 < n) { r.labels[a + lane + 64] = g1; r.scores[a + lane + 64] = fs1; }
-          if (lane == 0) {
-            slot->start = start;
-            slot->end = start + rlast;
-            slot->objective = score;
-          }
-        }
-      }
     }
-    if (lane == 0) { h->ibuf[3] = accepted; h->ibuf[4] = amb; }
+    if (lane == 0) { h->ibuf[3] = matches; h->ibuf[4] = start; h->ibuf[6] = rlast; }
   }
   __syncthreads();
-  const int accepted = h->ibuf[3];
-  *ambiguous = h->ibuf[4];
+  const int matches = h->ibuf[3];
+  const int start = h->ibuf[4];
+  const int rlast = h->ibuf[6];
+  const float score = h->fbuf[1];
   __syncthreads();
-  return accepted;
+  *ambiguous = matches > 1;
+  if (matches != 1 || !isfinite(score)) return 0;  // cu:129-139
+  if (wave == 0) {  // finish's label/score gather collapses to g and fs here
+    if (lane < n) { r.labels[a + lane] = g0; r.scores[a + lane] = fs0; }
+    if (lane + 64 < n) { r.labels[a + lane + 64] = g1; r.scores[a + lane + 64] = fs1; }
+    if (lane == 0) {
+      slot->start = start;
+      slot->end = start + rlast;
+      slot->objective = score;
+    }
+  }
+  return 1;
 }
 
 // ---------------------------------------------------------------------------
@@ -949,23 +1028,23 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) conventional_kernel(Param
   extern __shared__ __align__(16) unsigned char lds_raw[];
   const Lds L = carve(lds_raw, p);
   const int rec = blockIdx.x;
-  const RecordDesc d = p.desc[rec];
+  const RecordDesc d = load_pod(glb(p.desc) + rec);
   Rec r = make_rec(d, p, L);
   const Staged st = stage_tokens(d, p, rec, L, ALPHABET_NONE);
   if (threadIdx.x == 0) {
-    p.stitched[rec] = 0;
-    p.repair_passes[rec] = 0;
-    p.repaired_frames[rec] = 0;
-    for (int q = 0; q < 3; ++q) { p.shortcut_stats[3 * rec + q] = 0; p.routing_stats[3 * rec + q] = 0; }
+    glb(p.stitched)[rec] = 0;
+    glb(p.repair_passes)[rec] = 0;
+    glb(p.repaired_frames)[rec] = 0;
+    for (int q = 0; q < 3; ++q) { glb(p.shortcut_stats)[3 * rec + q] = 0; glb(p.routing_stats)[3 * rec + q] = 0; }
   }
   if (st.status >= 2) {
-    if (threadIdx.x == 0) { p.status[rec] = st.status; p.objective[rec] = NEG_INF; }
+    if (threadIdx.x == 0) { glb(p.status)[rec] = st.status; glb(p.objective)[rec] = NEG_INF; }
     write_failed(r, 0, r.T);
     return;
   }
   const DPOut o = dp_interval<K, D>(r, L, 0, r.T, true, nullptr, 1, nullptr, TRACE_IF_FINITE);
   const bool ok = isfinite(o.score);
-  if (threadIdx.x == 0) { p.status[rec] = ok ? 0 : 1; p.objective[rec] = o.score; }  // cu:507-510
+  if (threadIdx.x == 0) { glb(p.status)[rec] = ok ? 0 : 1; glb(p.objective)[rec] = o.score; }  // cu:507-510
   if (!ok) write_failed(r, 0, r.T);
 }
 
@@ -984,10 +1063,11 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
   const Lds L = carve(lds_raw, p);
   const int slot_index = xcd_slot(blockIdx.x, p.total_slots);
   if (slot_index >= p.total_slots) return;
-  const int rec = p.slot_record[slot_index];
-  const RecordDesc d = p.desc[rec];
+  const SlotEntry se = load_pod(glb(p.slot_entries) + slot_index);
+  const int rec = se.record;
+  const int chunk = se.chunk;
+  const RecordDesc d = load_pod(glb(p.desc) + rec);
   const Rec r = make_rec(d, p, L);
-  const int chunk = slot_index - d.chunk_offset;
   const int64_t a = (int64_t)chunk * p.H;
   const int64_t b = min(r.T, a + p.H);
   const int n = (int)(b - a);
@@ -995,17 +1075,17 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
   // Issue the chunk's emission rows first so their latency overlaps target
   // staging: for V <= 32, lane l of wave 0 loads rows a+l and a+64+l.
   const bool fast = p.mode == 2 && d.vocab <= 32 && (d.vocab & 3) == 0 &&
-                    (reinterpret_cast<uintptr_t>(d.emissions) & 15) == 0 && n <= 128;
+                    (reinterpret_cast<uintptr_t>(se.rows) & 15) == 0 && n <= 128;
   float row0[32], row1[32];
 #pragma unroll
   for (int c = 0; c < 32; ++c) { row0[c] = NEG_INF; row1[c] = NEG_INF; }
   if (fast && tid < 64) {
     auto load_row = [&](int f, float (&row)[32]) {
-      const float4* src = reinterpret_cast<const float4*>(d.emissions + (a + f) * (int64_t)d.vocab);
+      const GLB v4f_t* src = (const GLB v4f_t*)(glb(se.rows) + f * (int64_t)d.vocab);
 #pragma unroll
       for (int q = 0; q < 8; ++q)
         if (4 * q < d.vocab) {
-          const float4 v = src[q];
+          const v4f_t v = src[q];
           row[4 * q] = v.x; row[4 * q + 1] = v.y; row[4 * q + 2] = v.z; row[4 * q + 3] = v.w;
         }
     };
@@ -1013,13 +1093,13 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
     if (tid + 64 < n) load_row(tid + 64, row1);
   }
   const Staged st = stage_tokens(d, p, rec, L, p.mode != 2 ? ALPHABET_NONE : (fast ? ALPHABET_MASK32 : ALPHABET_BITMAP));
-  Slot* slot = p.slots + slot_index;
+  GLB Slot* slot = glb(p.slots) + slot_index;
   if (st.status >= 2) {  // rejected before any label-indexed read (cu:36, cu:642-652)
     write_failed(r, a, b);
     if (tid == 0) {
       Slot s{};
       s.a = (int)a; s.b = (int)b; s.objective = NEG_INF; s.status = (int16_t)st.status;
-      *slot = s;
+      store_pod(slot, s);
     }
     return;
   }
@@ -1028,7 +1108,7 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
     accepted = fast ? greedy_wave(r, L, a, b, st.alpha32, row0, row1, slot, &ambiguous)
                     : greedy_chunk(r, L, a, b, slot, &ambiguous);
   if (!accepted) {  // initial chunk DP (cu:721-726), relaxed init for a > 0
-    float* fr = r.frontier ? r.frontier + (int64_t)chunk * r.S : nullptr;
+    GLB float* fr = r.frontier ? r.frontier + (int64_t)chunk * r.S : nullptr;
     const DPOut o = dp_interval<K, D>(r, L, a, b, b == r.T, nullptr, a + 1, fr, TRACE_ALWAYS);
     if (tid == 0) {
       slot->objective = o.score;
@@ -1050,35 +1130,28 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
 // rounds, seam validation, full-DP fallback, final path and every per-record
 // output (plan_repairs cu:164-228, repair DP cu:727-760, validate_seams
 // cu:562-592, fallback_recurrence cu:552-559, finish cu:642-667).
-template <int K, int D>
-__global__ void __launch_bounds__(K == 32 ? 640 : 256) tail_kernel(Params p) {
-  extern __shared__ __align__(16) unsigned char lds_raw[];
-  const Lds L = carve(lds_raw, p);
+__device__ inline Slot load_slot(const Slot* x) { return *x; }
+__device__ inline Slot load_slot(const GLB Slot* x) { return load_pod(x); }
+
+// The tail of one record; SP is the slot array, in LDS or in global memory.
+template <int K, int D, class SP>
+__device__ __attribute__((always_inline)) void tail_body(const Params& p, const RecordDesc& d, int rec, const Rec& r,
+                                                      const Lds& L, SP sl, bool in_lds) {
   Header* h = L.h;
-  const int rec = blockIdx.x;
-  const RecordDesc d = p.desc[rec];
-  const Rec r = make_rec(d, p, L);
   const int tid = threadIdx.x;
   const int64_t T = r.T;
   const int n = (int)(1 + (T - 1) / p.H);
-  Slot* gs = p.slots + d.chunk_offset;
-  Slot* sl = gs;
-  if (n <= p.lds_tail_slots) {
-    for (int c = tid; c < n; c += blockDim.x) L.tslots[c] = gs[c];
-    __syncthreads();
-    sl = L.tslots;
-  }
   const int status0 = sl[0].status;
   if (status0 >= 2) {
     if (tid == 0) {
-      p.status[rec] = status0;
-      p.objective[rec] = NEG_INF;
-      p.stitched[rec] = 0;
-      p.repair_passes[rec] = 0;
-      p.repaired_frames[rec] = 0;
-      for (int q = 0; q < 3; ++q) { p.shortcut_stats[3 * rec + q] = 0; p.routing_stats[3 * rec + q] = 0; }
+      glb(p.status)[rec] = status0;
+      glb(p.objective)[rec] = NEG_INF;
+      glb(p.stitched)[rec] = 0;
+      glb(p.repair_passes)[rec] = 0;
+      glb(p.repaired_frames)[rec] = 0;
+      for (int q = 0; q < 3; ++q) { glb(p.shortcut_stats)[3 * rec + q] = 0; glb(p.routing_stats)[3 * rec + q] = 0; }
       if (p.reuse_stats)
-        for (int q = 0; q < 4; ++q) p.reuse_stats[4 * rec + q] = 0;
+        for (int q = 0; q < 4; ++q) glb(p.reuse_stats)[4 * rec + q] = 0;
     }
     return;
   }
@@ -1090,11 +1163,11 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) tail_kernel(Params p) {
   // nothing (plan_repairs joins every neighbour and its budget preflight
   // proposes no region) and validate_seams stitches iff the fp32 total is
   // finite. Wave 0 checks all seams at once and writes the result.
-  if (n <= 64 && sl == L.tslots) {
+  if (n <= 64 && in_lds) {
     if (tid < 64) {
       const int k = tid;
       const bool valid = k < n;
-      const Slot sk = sl[valid ? k : 0];
+      const Slot sk = load_slot(sl + (valid ? k : 0));
       const int end_prev = (valid && k > 0) ? sl[k - 1].end : 0;
       const bool ok = !valid || (isfinite(sk.objective) && (k == 0 || legal_seam(r, sk.start, end_prev)));
       int done = 0;
@@ -1110,17 +1183,17 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) tail_kernel(Params p) {
 #pragma unroll
           for (int off = 32; off > 0; off >>= 1) frames += __shfl_xor(frames, off, 64);
           if (tid == 0) {
-            p.status[rec] = 0;
-            p.objective[rec] = total;
-            p.stitched[rec] = 1;
-            p.repair_passes[rec] = 0;
-            p.repaired_frames[rec] = 0;
-            p.shortcut_stats[3 * rec + 0] = __popcll(shortcut);
-            p.shortcut_stats[3 * rec + 1] = frames;
-            p.shortcut_stats[3 * rec + 2] = __popcll(amb);
-            for (int q = 0; q < 3; ++q) p.routing_stats[3 * rec + q] = 0;
+            glb(p.status)[rec] = 0;
+            glb(p.objective)[rec] = total;
+            glb(p.stitched)[rec] = 1;
+            glb(p.repair_passes)[rec] = 0;
+            glb(p.repaired_frames)[rec] = 0;
+            glb(p.shortcut_stats)[3 * rec + 0] = __popcll(shortcut);
+            glb(p.shortcut_stats)[3 * rec + 1] = frames;
+            glb(p.shortcut_stats)[3 * rec + 2] = __popcll(amb);
+            for (int q = 0; q < 3; ++q) glb(p.routing_stats)[3 * rec + q] = 0;
             if (p.reuse_stats) {
-              int64_t* u = p.reuse_stats + 4 * rec;
+              GLB int64_t* u = glb(p.reuse_stats) + 4 * rec;
               u[0] = 0; u[1] = 0; u[2] = frontier_on ? (int64_t)__popcll(dp) * S : 0; u[3] = 0;
             }
           }
@@ -1204,7 +1277,7 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) tail_kernel(Params p) {
     __syncthreads();
     if (p.overlap && early) {
       if (early == 1) {  // early full fallback (repair_recurrence, cu:535-550)
-        const Slot s0 = sl[0];
+        const Slot s0 = load_slot(sl + (0));
         const bool resume = frontier_on && s0.frontier_end > 0 && s0.frontier_end <= T;
         if (resume) { reuse1 += s0.frontier_end; reuse3 += S; }
         const DPOut o = dp_interval<K, D>(r, L, 0, T, true, resume ? r.frontier : nullptr,
@@ -1217,11 +1290,11 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) tail_kernel(Params p) {
       }
     } else {
       for (int k = 0; k < n; ++k) {  // repair DP over merged intervals (cu:727-760)
-        const Slot s = sl[k];
+        const Slot s = load_slot(sl + (k));
         if (s.a >= s.b || (repairs && !s.flag)) continue;
         bool resume = false;
         int64_t start_t = s.a + 1;
-        float* fr = frontier_on ? r.frontier + (int64_t)k * S : nullptr;
+        GLB float* fr = frontier_on ? r.frontier + (int64_t)k * S : nullptr;
         if (frontier_on) {
           if (s.frontier_end > s.a && s.frontier_end <= s.b) {
             resume = true;
@@ -1268,7 +1341,7 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) tail_kernel(Params p) {
     objective = h->fbuf[2];
     __syncthreads();
     if (!stitched) {  // fallback_recurrence, cu:552-559
-      const Slot s0 = sl[0];
+      const Slot s0 = load_slot(sl + (0));
       const bool resume = frontier_on && s0.frontier_end > 0 && s0.frontier_end <= T;
       if (resume) { reuse1 += s0.frontier_end; reuse3 += S; }
       const DPOut o = dp_interval<K, D>(r, L, 0, T, true, resume ? r.frontier : nullptr,
@@ -1279,29 +1352,48 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) tail_kernel(Params p) {
   }
   if (status != 0) write_failed(r, 0, T);
   if (tid == 0) {
-    p.status[rec] = status;
-    p.objective[rec] = objective;
-    p.stitched[rec] = stitched;
-    p.repair_passes[rec] = passes;
-    p.repaired_frames[rec] = repaired;
-    p.shortcut_stats[3 * rec + 0] = sc_accepted;
-    p.shortcut_stats[3 * rec + 1] = sc_frames;
-    p.shortcut_stats[3 * rec + 2] = sc_ambiguous;
-    p.routing_stats[3 * rec + 0] = early;
-    p.routing_stats[3 * rec + 1] = rejected;
-    p.routing_stats[3 * rec + 2] = maxprop;
+    glb(p.status)[rec] = status;
+    glb(p.objective)[rec] = objective;
+    glb(p.stitched)[rec] = stitched;
+    glb(p.repair_passes)[rec] = passes;
+    glb(p.repaired_frames)[rec] = repaired;
+    glb(p.shortcut_stats)[3 * rec + 0] = sc_accepted;
+    glb(p.shortcut_stats)[3 * rec + 1] = sc_frames;
+    glb(p.shortcut_stats)[3 * rec + 2] = sc_ambiguous;
+    glb(p.routing_stats)[3 * rec + 0] = early;
+    glb(p.routing_stats)[3 * rec + 1] = rejected;
+    glb(p.routing_stats)[3 * rec + 2] = maxprop;
     if (p.reuse_stats) {
-      int64_t* u = p.reuse_stats + 4 * rec;
+      GLB int64_t* u = glb(p.reuse_stats) + 4 * rec;
       u[0] = reuse0; u[1] = reuse1; u[2] = reuse2; u[3] = reuse3;
     }
+  }
+}
+
+template <int K, int D>
+__global__ void __launch_bounds__(K == 32 ? 640 : 256) tail_kernel(Params p) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  const Lds L = carve(lds_raw, p);
+  const int rec = blockIdx.x;
+  const RecordDesc d = load_pod(glb(p.desc) + rec);
+  const Rec r = make_rec(d, p, L);
+  const int n = (int)(1 + (r.T - 1) / p.H);
+  GLB Slot* gs = glb(p.slots) + d.chunk_offset;
+  if (n <= p.lds_tail_slots) {
+    Slot* ls = reinterpret_cast<Slot*>(lds_raw + ((uintptr_t)L.tslots - (uintptr_t)lds_raw));
+    for (int c = threadIdx.x; c < n; c += blockDim.x) ls[c] = load_pod(gs + c);
+    __syncthreads();
+    tail_body<K, D>(p, d, rec, r, L, ls, true);
+  } else {
+    tail_body<K, D>(p, d, rec, r, L, gs, false);
   }
 }
 
 // One workgroup per record: any NaN or +inf rejects it (cu:881-891).
 __global__ void __launch_bounds__(1024) validity_kernel(const int64_t* desc, uint8_t* valid) {
   const int rec = blockIdx.x;
-  const float* values = reinterpret_cast<const float*>(desc[2 * rec]);
-  const int64_t n = desc[2 * rec + 1];
+  const GLB float* values = (const GLB float*)(glb(desc)[2 * rec]);
+  const int64_t n = glb(desc)[2 * rec + 1];
   int bad = 0;
   const uintptr_t addr = reinterpret_cast<uintptr_t>(values);
   int64_t head = (int64_t)(((16 - (addr & 15)) & 15) / 4);
@@ -1310,10 +1402,10 @@ __global__ void __launch_bounds__(1024) validity_kernel(const int64_t* desc, uin
     const float v = values[i];
     bad |= isnan(v) || v == INFINITY;
   }
-  const float4* v4 = reinterpret_cast<const float4*>(values + head);
+  const GLB v4f_t* v4 = (const GLB v4f_t*)(values + head);
   const int64_t n4 = (n - head) / 4;
   for (int64_t i = threadIdx.x; i < n4; i += blockDim.x) {
-    const float4 v = v4[i];
+    const v4f_t v = v4[i];
     bad |= isnan(v.x) || v.x == INFINITY || isnan(v.y) || v.y == INFINITY ||
            isnan(v.z) || v.z == INFINITY || isnan(v.w) || v.w == INFINITY;
   }
@@ -1322,7 +1414,7 @@ __global__ void __launch_bounds__(1024) validity_kernel(const int64_t* desc, uin
     bad |= isnan(v) || v == INFINITY;
   }
   bad = __syncthreads_or(bad);
-  if (threadIdx.x == 0) valid[rec] = bad ? 0 : 1;
+  if (threadIdx.x == 0) glb(valid)[rec] = bad ? 0 : 1;
 }
 
 }  // namespace ffa
@@ -1475,7 +1567,7 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
   const int64_t tail_slots = optimized ? std::min<int64_t>(n_max, ffa::TAIL_SLOT_CAP) : 0;
   const int64_t greedy_bytes = 20 * align_up(H, 32) + 2048 + align_up(2 * d_cap, 16) + 8 * v_words;
   const int64_t region = std::max(greedy_bytes, 32 * tail_slots);
-  const int64_t lds = align_up((int64_t)sizeof(ffa::Header), 16) + align_up(2 * std::max<int64_t>(u_max, 1), 16) + region;
+  const int64_t lds = align_up((int64_t)sizeof(ffa::Header), 16) + align_up(2 * (std::max<int64_t>(u_max, 1) + ffa::YTOK_PAD), 16) + region;
   if (lds > 64 * 1024) return fail(FFA_E_INVALID, "batch needs more than 64 KiB of LDS per workgroup");
   int64_t ws = align_up(4 * bp_words, 256);
   const int64_t ws_slots = ws;
@@ -1485,7 +1577,7 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
   std::memset(plan, 0, sizeof(*plan));
   plan->count = count;
   plan->total_frames = total_frames;
-  plan->table_bytes = count * (int64_t)sizeof(ffa::RecordDesc) + 4 * slots;
+  plan->table_bytes = count * (int64_t)sizeof(ffa::RecordDesc) + (int64_t)sizeof(ffa::SlotEntry) * slots;
   plan->workspace_bytes = std::max<int64_t>(ws, 256);
   plan->reuse_rows = frontier ? count : 0;
   int64_t* in = plan->internal;
@@ -1518,7 +1610,7 @@ int ffa_align_describe(const ffa_align_plan* plan, const ffa_record* records, vo
   const bool frontier = in[I_FRONTIER] != 0;
   const int64_t H = in[I_H];
   auto* desc = static_cast<ffa::RecordDesc*>(host_table);
-  auto* slot_record = reinterpret_cast<int32_t*>(desc + count);
+  auto* entries = reinterpret_cast<ffa::SlotEntry*>(desc + count);
   int64_t frame = 0, bp = 0, fr = 0;
   int32_t slot = 0;
   for (int64_t i = 0; i < count; ++i) {
@@ -1543,7 +1635,11 @@ int ffa_align_describe(const ffa_align_plan* plan, const ffa_record* records, vo
     frame += r.frames;
     bp += r.frames * stride_of(S);
     if (optimized) {
-      for (int64_t c = 0; c < n; ++c) slot_record[slot + c] = (int32_t)i;
+      for (int64_t c = 0; c < n; ++c) {
+        entries[slot + c].rows = r.emissions + c * H * r.vocab;
+        entries[slot + c].record = (int32_t)i;
+        entries[slot + c].chunk = (int32_t)c;
+      }
       slot += (int32_t)n;
     }
   }
@@ -1564,7 +1660,7 @@ extern "C" int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_opti
   if (o->mode != in[I_MODE] || o->chunk_frames != in[I_H]) return fail(FFA_E_INVALID, "options differ from the plan");
   ffa::Params p{};
   p.desc = static_cast<const ffa::RecordDesc*>(device_table);
-  p.slot_record = reinterpret_cast<const int32_t*>(p.desc + plan->count);
+  p.slot_entries = reinterpret_cast<const ffa::SlotEntry*>(p.desc + plan->count);
   p.validity = emission_validity;
   p.labels = out->labels;
   p.scores = out->scores;

@@ -64,9 +64,9 @@ std::tuple<std::vector<at::Tensor>, std::vector<int64_t>> align(
     bool overlap_fallback, int64_t trace_min_frames, int64_t repair_min_frames, bool frontier_reuse,
     int64_t frontier_min_frames, const std::optional<at::Tensor>& emission_validity, bool check_inputs) {
   const int64_t count = emissions.size();
-  TORCH_CHECK(count > 0 && count <= FFA_MAX_BATCH && (int64_t)targets.size() == count &&
-                  (int64_t)blanks.size() == count,
-              "batch must contain 1..65535 matching emissions, targets and blanks");
+  TORCH_CHECK_VALUE(count > 0 && count <= FFA_MAX_BATCH && (int64_t)targets.size() == count,
+                    "provide 1..65535 matching emissions and targets");
+  TORCH_CHECK_VALUE((int64_t)blanks.size() == count, "provide one blank ID per record");
   TORCH_CHECK(emissions[0].is_cuda(), "CUDA emissions required");
   const auto device = emissions[0].device();
   c10::hip::HIPGuardMasqueradingAsCUDA guard(device);
@@ -74,9 +74,9 @@ std::tuple<std::vector<at::Tensor>, std::vector<int64_t>> align(
   const uint8_t* mask = nullptr;
   if (emission_validity.has_value()) {
     const auto& m = *emission_validity;
-    TORCH_CHECK(m.device() == device && m.scalar_type() == at::kBool && m.dim() == 1 && m.numel() == count &&
-                    m.is_contiguous(),
-                "emission_validity must be contiguous CUDA bool [batch] on the input device");
+    TORCH_CHECK_VALUE(m.device() == device && m.scalar_type() == at::kBool && m.dim() == 1 && m.numel() == count &&
+                          m.is_contiguous(),
+                      "emission_validity must be contiguous CUDA bool [batch] on the input device");
     recordStreamMasqueradingAsCUDA(m.storage().data_ptr(), stream);
     mask = reinterpret_cast<const uint8_t*>(m.data_ptr<bool>());
   }
@@ -103,10 +103,14 @@ std::tuple<std::vector<at::Tensor>, std::vector<int64_t>> align(
   for (int64_t i = 0; i < count; ++i) {
     const auto& e = emissions[i];
     const auto& t = targets[i];
-    TORCH_CHECK(e.device() == device && t.device() == device && e.scalar_type() == at::kFloat &&
-                    t.scalar_type() == at::kLong && e.dim() == 2 && t.dim() == 1 && e.is_contiguous() &&
-                    t.is_contiguous(),
-                "resident inputs must be contiguous FP32 [T,V] and int64 [U] on one CUDA device");
+    // the per-record metadata contract of alignment.py:243-251, raised as ValueError
+    TORCH_CHECK_VALUE(e.is_cuda() && e.device() == device && t.device() == device && e.scalar_type() == at::kFloat &&
+                          t.scalar_type() == at::kLong && e.dim() == 2 && t.dim() == 1 && e.is_contiguous() &&
+                          t.is_contiguous(),
+                      "inputs must be contiguous CUDA float32 [T,V] and int64 [U] on one device");
+    TORCH_CHECK_VALUE(e.size(0) > 0 && e.size(0) <= INT_MAX && e.size(1) > 0 && e.size(1) <= FFA_MAX_VOCAB &&
+                          2 * t.numel() + 1 <= FFA_MAX_STATES && blanks[i] >= 0 && blanks[i] < e.size(1),
+                      "unsupported frame count, vocabulary, target length, or blank ID");
     records[i].emissions = e.data_ptr<float>();
     records[i].targets = t.numel() ? t.data_ptr<int64_t>() : nullptr;
     records[i].frames = e.size(0);

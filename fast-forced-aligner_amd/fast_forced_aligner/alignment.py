@@ -154,6 +154,22 @@ def _metadata(emissions: Sequence[Tensor], targets: Sequence[Tensor],
 MAX_TOKENS = 10239
 
 
+def _blank_list(emissions: Sequence[Tensor], targets: Sequence[Tensor],
+                blank_id: int | Sequence[int]) -> list[int]:
+    """The O(1)-per-record part of ``_metadata``: batch size and blank types."""
+    count = len(emissions)
+    if not 0 < count <= 65535 or len(targets) != count:
+        raise ValueError("provide 1..65535 matching emissions and targets")
+    if type(blank_id) is int:
+        return [blank_id] * count
+    blanks = list(blank_id)
+    if len(blanks) != count:
+        raise ValueError("provide one blank ID per record")
+    if not all(type(b) is int for b in blanks):
+        raise ValueError("unsupported frame count, vocabulary, target length, or blank ID")
+    return blanks
+
+
 @torch.inference_mode()
 def validate_inputs(emissions: Sequence[Tensor], targets: Sequence[Tensor], *,
                     blank_id: int | Sequence[int] = 0) -> None:
@@ -221,7 +237,12 @@ def align(emissions: Sequence[Tensor], targets: Sequence[Tensor], *,
         raise ValueError("mode must be 'optimized' or 'conventional'")
     if type(check_inputs) is not bool:
         raise TypeError("check_inputs must be bool")
-    blanks = _metadata(emissions, targets, blank_id)
+    if emissions and isinstance(emissions[0], Tensor) and emissions[0].is_cuda:
+        # The native operator checks every record's metadata with the same
+        # messages and raises ValueError (O(B) in C++ instead of Python).
+        blanks = _blank_list(emissions, targets, blank_id)
+    else:
+        blanks = _metadata(emissions, targets, blank_id)
     if emission_validity is not None:
         if (not isinstance(emission_validity, Tensor)
                 or emission_validity.device != emissions[0].device
@@ -229,14 +250,13 @@ def align(emissions: Sequence[Tensor], targets: Sequence[Tensor], *,
                 or emission_validity.numel() != len(emissions)
                 or not emission_validity.is_contiguous()):
             raise ValueError("emission_validity must be contiguous CUDA bool [batch] on the input device")
-    with torch.cuda.device(emissions[0].device):
-        load_extension()
-        optimized = mode == "optimized"
-        # the fixed knob vector of py:496-501
-        tensors, lengths = torch.ops.fast_forced_aligner_cuda.align(
-            list(emissions), list(targets), blanks,
-            128, 2 if optimized else 0, 512, 2, 2, 2,
-            512 if optimized else 0, 0, False, True, optimized,
-            2048, 2048, optimized, 2048, emission_validity, check_inputs,
-        )
+    load_extension()
+    optimized = mode == "optimized"
+    # the fixed knob vector of py:496-501; the operator guards the input device
+    tensors, lengths = torch.ops.fast_forced_aligner_cuda.align(
+        list(emissions), list(targets), blanks,
+        128, 2 if optimized else 0, 512, 2, 2, 2,
+        512 if optimized else 0, 0, False, True, optimized,
+        2048, 2048, optimized, 2048, emission_validity, check_inputs,
+    )
     return AlignmentBatch(tuple(lengths), *tensors)
