@@ -66,15 +66,22 @@ struct Slot {  // per-chunk state of optimized mode (cu:1021-1029 buffers), 32 b
 };
 static_assert(sizeof(Slot) == 32, "slot layout");
 
-struct SlotEntry {  // per-chunk table entry: the chunk's first emission row and owner
-  const float* rows;
-  int32_t record, chunk;
+// Per-chunk descriptor of optimized mode: everything the greedy fast path
+// needs, so a workgroup starts with one scalar load and no dependent lookups.
+struct ChunkDesc {
+  const float* rows;        // first emission row of the chunk
+  const int64_t* targets;   // the record's targets
+  int64_t out;              // index of the chunk's first frame in labels / scores
+  int32_t frames, tokens, vocab, blank;  // T, U, V, blank of the record
+  int32_t record, chunk, n, flags;       // n = frames in this chunk; flags: CHUNK_*
+  int32_t nchunks, first_slot;           // the record's chunk count and first slot
 };
-static_assert(sizeof(SlotEntry) == 16, "slot entry layout");
+static_assert(sizeof(ChunkDesc) == 64, "chunk descriptor layout");
+enum { CHUNK_FAST = 1 };  // V <= 32, V % 4 == 0, 16-byte aligned rows, n <= 128, greedy on
 
 struct Params {
   const RecordDesc* desc;
-  const SlotEntry* slot_entries;
+  const ChunkDesc* chunks;
   const uint8_t* validity;
   int64_t* labels;
   float* scores;
@@ -91,7 +98,7 @@ struct Params {
   float* frontiers;
   int64_t budget, repair_min, frontier_min;
   int32_t count, total_slots, H, mode, repair_rounds, check_inputs, overlap, frontier_batch;
-  int32_t u_cap, d_cap, v_words, lds_greedy, lds_tail_slots;
+  int32_t u_cap, d_cap, v_words, lds_tail_slots;
 };
 
 // ---------------------------------------------------------------------------
@@ -106,11 +113,17 @@ struct Header {
   float term_v[2];
   int ibuf[8];
   float fbuf[4];
+  int stg_f[16];       // per-wave staging flags: 1 out-of-vocabulary id, 2 blank id among the targets
+  int stg_r[16];       // per-wave adjacent-repeat counts
+  uint32_t stg_m[16];  // per-wave alphabet masks (V <= 32)
+  int gbad[2];         // per-wave greedy rejection (fast path)
+  int last;            // the record's outputs are written (tail fast path)
 };
 
 struct Lds {
   Header* h;
-  int16_t* ytok;  // targets as int16 (V <= 8192)
+  int16_t* ytok;   // targets as int16 (V <= 8192)
+  uint16_t* key3;  // per target position j: key of y[j], y[j+1], y[j+2] (placement prefilter)
   // greedy region (aliased by the tail's slot copy)
   int32_t* g;
   float* fs;
@@ -127,6 +140,10 @@ struct Lds {
 
 __device__ inline size_t align16(size_t x) { return (x + 15) & ~size_t(15); }
 
+// Entries of the per-frame greedy arrays: H rounded up to 32, at least 128
+// (the fast path indexes them by lane across two waves).
+__host__ __device__ inline int64_t greedy_frames(int64_t H) { return H < 128 ? 128 : (H + 31) & ~int64_t(31); }
+
 __device__ inline Lds carve(unsigned char* base, const Params& p) {
   Lds L;
   size_t off = 0;
@@ -134,9 +151,11 @@ __device__ inline Lds carve(unsigned char* base, const Params& p) {
   off = align16(sizeof(Header));
   L.ytok = reinterpret_cast<int16_t*>(base + off);
   off = align16(off + 2 * ((size_t)p.u_cap + YTOK_PAD));
+  L.key3 = reinterpret_cast<uint16_t*>(base + off);
+  off = align16(off + 2 * ((size_t)p.u_cap + YTOK_PAD));
   unsigned char* region = base + off;
   size_t g = 0;
-  const size_t h32 = (size_t)((p.H + 31) & ~31);
+  const size_t h32 = (size_t)greedy_frames(p.H);
   L.g = reinterpret_cast<int32_t*>(region + g); g += 4 * h32;
   L.fs = reinterpret_cast<float*>(region + g); g += 4 * h32;
   L.r = reinterpret_cast<int32_t*>(region + g); g += 4 * h32;
@@ -222,9 +241,30 @@ __device__ inline uint32_t lanes_below(uint64_t mask) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
+// Sequential fp32 sum ((x0 + x1) + x2) + ... of 128 LDS values by one thread:
+// 16-byte reads issued ahead of the dependent chain of adds.
+__device__ __attribute__((always_inline)) inline float serial_sum128(const float* x) {
+  const v4f_t* x4 = reinterpret_cast<const v4f_t*>(x);
+  float acc = 0.0f;
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    v4f_t v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = x4[16 * half + i];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      acc = (half == 0 && i == 0) ? v[i].x : acc + v[i].x;
+      acc += v[i].y;
+      acc += v[i].z;
+      acc += v[i].w;
+    }
+  }
+  return acc;
+}
+
 // Sequential fp32 sum ((x0 + x1) + x2) + ... of an LDS array by one thread,
 // reading 32 values ahead of the dependent adds. x must hold a multiple of 32.
-__device__ inline float serial_sum(const float* x, int n) {
+__device__ __attribute__((always_inline)) inline float serial_sum(const float* x, int n) {
   float acc = x[0];
   for (int base = 0; base < n; base += 32) {
     float v[32];
@@ -590,25 +630,57 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
 struct Staged {
   int status;
   uint32_t alpha32;
+  int blank_in;  // some in-vocabulary target equals the blank id (only reachable unchecked)
 };
 
 enum { ALPHABET_NONE = 0, ALPHABET_MASK32 = 1, ALPHABET_BITMAP = 2 };
 
-__device__ Staged stage_tokens(const RecordDesc& d, const Params& p, int rec, const Lds& L, int alphabet) {
+template <int CTRL, int ROW_MASK>
+__device__ inline int dpp_or(int v) {
+  return v | __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, false);
+}
+
+// Wave64 inclusive OR-scan (same DPP pattern as wave_scan_dpp); lane 63 holds
+// the OR of all lanes.
+__device__ inline int wave_or_scan_dpp(int x) {
+  x = dpp_or<0x111, 0xf>(x);
+  x = dpp_or<0x112, 0xf>(x);
+  x = dpp_or<0x114, 0xf>(x);
+  x = dpp_or<0x118, 0xf>(x);
+  x = dpp_or<0x142, 0xa>(x);
+  x = dpp_or<0x143, 0xc>(x);
+  return x;
+}
+
+// Prefilter key of three consecutive targets: exact for V <= 32 (5 bits each),
+// a 16-bit hash otherwise (candidates are always verified token by token).
+__device__ inline uint32_t tri_key(int x0, int x1, int x2, bool small) {
+  return small ? ((uint32_t)(x0 & 31) | (uint32_t)(x1 & 31) << 5 | (uint32_t)(x2 & 31) << 10)
+               : (((uint32_t)x0 * 40503u + (uint32_t)x1 * 30011u + (uint32_t)x2 * 52511u) & 0xffffu);
+}
+
+// Target staging and validation (pack_inputs, cu:819-877), done by every
+// workgroup that needs the record: copies the targets into LDS as int16,
+// computes the status and the transcript alphabet (cu:53-58). For V <= 32 the
+// alphabet is returned as a bit mask; otherwise it is left in L.bitmap. With
+// `keys`, the placement prefilter keys of every target position are built too.
+// Out-of-vocabulary ids are rejected (status 3) even unchecked: the reference
+// reads out of bounds there (py:400-402); this build never reads outside the
+// emission rows. One workgroup barrier.
+__device__ __attribute__((always_inline)) Staged stage_targets(const GLB int64_t* y, int U, int V, int blank, int64_t T, int rec,
+                                const Params& p, const Lds& L, int alphabet, bool keys) {
   Header* h = L.h;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
-  const int V = d.vocab;
   if (alphabet == ALPHABET_BITMAP) {
     for (int w = tid; w < (V + 31) / 32; w += blockDim.x) L.bitmap[w] = 0;
     __syncthreads();
-    if (tid == 0) atomicOr(&L.bitmap[d.blank >> 5], 1u << (d.blank & 31));
+    if (tid == 0) atomicOr(&L.bitmap[blank >> 5], 1u << (blank & 31));
   }
-  int oov = 0, invalid = 0, repeats = 0;
+  bool oov = false, bin = false;
+  int repeats = 0;
   uint32_t mask = 0;
   // thread t checks targets [t*per, (t+1)*per) and compares its first one with
   // the target before it: one batch of loads in flight per thread
-  const GLB int64_t* y = glb(d.targets);
-  const int U = d.tokens;
   const int per = (U + (int)blockDim.x - 1) / (int)blockDim.x;
   const int j0 = tid * per, j1 = min(U, j0 + per);
   int64_t before = (j0 > 0 && j0 < U) ? y[j0 - 1] : 0;
@@ -623,7 +695,7 @@ __device__ Staged stage_tokens(const RecordDesc& d, const Params& p, int rec, co
         const int64_t tok = v[q];
         const bool out = tok < 0 || tok >= V;  // checked as int64 before narrowing (cu:860)
         oov |= out;
-        invalid |= out || tok == d.blank;
+        bin |= !out && tok == blank;
         repeats += j > 0 && tok == before;  // cu:861
         before = tok;
         L.ytok[j] = (int16_t)(out ? 0 : tok);
@@ -636,40 +708,101 @@ __device__ Staged stage_tokens(const RecordDesc& d, const Params& p, int rec, co
   }
   // sentinel padding after the targets: the placement prefilter reads ahead
   for (int j = U + tid; j < U + YTOK_PAD; j += blockDim.x) L.ytok[j] = -1;
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {  // one reduction for all four values
-    oov |= __shfl_xor(oov, off, 64);
-    invalid |= __shfl_xor(invalid, off, 64);
-    repeats += __shfl_xor(repeats, off, 64);
-    mask |= (uint32_t)__shfl_xor((int)mask, off, 64);
-  }
+  // wave reductions: ballots for the flags, DPP scans for the count and the mask
+  const int wf = (__ballot(oov) != 0 ? 1 : 0) | (__ballot(bin) != 0 ? 2 : 0);
+  const int wr = __builtin_amdgcn_readlane(wave_scan_dpp(repeats), 63);
+  const int wm = __builtin_amdgcn_readlane(wave_or_scan_dpp((int)mask), 63);
   if (lane == 0) {
-    h->red_i[wave] = oov | (invalid << 1);
-    h->red_j[wave] = repeats;
-    h->red_m[wave] = mask;
+    h->stg_f[wave] = wf;
+    h->stg_r[wave] = wr;
+    h->stg_m[wave] = (uint32_t)wm;
   }
   __syncthreads();
   int flags = 0, reps = 0;
-  uint32_t m = alphabet == ALPHABET_MASK32 ? 1u << d.blank : 0u;
+  uint32_t m = alphabet == ALPHABET_MASK32 ? 1u << blank : 0u;
   for (int w = 0; w < nw; ++w) {
-    flags |= h->red_i[w];
-    reps += h->red_j[w];
-    m |= h->red_m[w];
+    flags |= h->stg_f[w];
+    reps += h->stg_r[w];
+    m |= h->stg_m[w];
   }
-  __syncthreads();
+  if (keys) {
+    const bool small = V <= 32;
+    for (int j = j0; j < j1; ++j) L.key3[j] = (uint16_t)tri_key(L.ytok[j], L.ytok[j + 1], L.ytok[j + 2], small);
+  }
   Staged st;
   st.alpha32 = m;
+  st.blank_in = (flags & 2) ? 1 : 0;
   if (flags & 1) st.status = 3;
-  else if (p.check_inputs && (flags & 2)) st.status = 3;                          // cu:872
-  else if (p.check_inputs && (int64_t)d.tokens + reps > d.frames) st.status = 4;  // cu:873
-  else st.status = (p.validity && !glb(p.validity)[rec]) ? 2 : 0;               // cu:836
+  else if (p.check_inputs && (flags & 2)) st.status = 3;                // cu:872
+  else if (p.check_inputs && (int64_t)U + reps > T) st.status = 4;      // cu:873
+  else st.status = (p.validity && !glb(p.validity)[rec]) ? 2 : 0;     // cu:836
   return st;
+}
+
+__device__ inline Staged stage_tokens(const RecordDesc& d, const Params& p, int rec, const Lds& L, int alphabet) {
+  return stage_targets(glb(d.targets), d.tokens, d.vocab, d.blank, d.frames, rec, p, L, alphabet, false);
 }
 
 __device__ inline bool legal_seam(const Rec& r, int start, int before) {  // cu:157-161
   const int jump = start - before;
   return jump == 0 || jump == 1 ||
          (jump == 2 && label_of(r, start) != r.blank && label_of(r, start) != label_of(r, start - 2));
+}
+
+// Literal placement test of the reference (cu:119-134), used when an
+// in-vocabulary target equals the blank id (reachable only with
+// check_inputs=False): the substring formulation below assumes blank labels sit
+// at even states only. Every start state is checked against every label change
+// of the chunk. Needs the greedy labels in L.g[0, n); fills L.pd / L.pc with the
+// change offsets and labels. Workgroup-wide; returns the number of legal
+// placements, *start (meaningful when exactly one) and *rlast.
+__device__ __attribute__((always_inline)) int place_literal(const Lds& L, const int16_t* ytok, int n, int S, int blank, bool at_start, bool at_end,
+                             int* start, int* rlast) {
+  Header* h = L.h;
+  const int tid = threadIdx.x, NT = blockDim.x;
+  int carry = 0;  // r | changes << 16
+  for (int base = 0; base < n; base += NT) {
+    const int f = base + tid;
+    int inc = 0, chg = 0;
+    if (f < n && f > 0) {
+      const int x = L.g[f], w = L.g[f - 1];
+      chg = x != w;
+      inc = x == w ? 0 : (x == blank || w == blank ? 1 : 2);  // cu:112-117
+    }
+    const int v = block_incl_scan(inc | (chg << 16), h) + carry;
+    if (f < n) {
+      L.r[f] = v & 0xffff;
+      if (chg) {
+        L.pd[v >> 16] = v & 0xffff;
+        L.pc[v >> 16] = L.g[f];
+      }
+    }
+    if (tid == NT - 1) h->ibuf[2] = v;
+    __syncthreads();
+    carry = h->ibuf[2];
+    __syncthreads();
+  }
+  const int segs = (carry >> 16) + 1;
+  const int rl = carry & 0xffff;
+  const int g0 = L.g[0];
+  if (tid == 0) h->ibuf[4] = -1;
+  __syncthreads();
+  int local = 0;
+  for (int s = tid; s < S; s += NT) {
+    const int ls = (s & 1) ? (int)ytok[s >> 1] : blank;
+    const int terminal = s + rl;
+    bool legal = ls == g0 && !(at_start && s > 1) && terminal < S && !(at_end && terminal < S - 2);
+    for (int k = 1; k < segs && legal; ++k) {
+      const int q = s + L.pd[k];
+      legal = ((q & 1) ? (int)ytok[q >> 1] : blank) == L.pc[k];
+    }
+    if (legal) { ++local; h->ibuf[4] = s; }
+  }
+  const int matches = block_sum(local, h);
+  *start = h->ibuf[4];
+  *rlast = rl;
+  __syncthreads();
+  return matches;
 }
 
 // ---------------------------------------------------------------------------
@@ -689,7 +822,7 @@ __device__ inline bool legal_seam(const Rec& r, int start, int before) {  // cu:
 // *ambiguous is set when more than one placement is legal.
 constexpr int CAND_CAP = 256;
 
-__device__ int greedy_chunk(const Rec& r, const Lds& L, int64_t a, int64_t b, GLB Slot* slot, int* ambiguous) {
+__device__ __attribute__((always_inline)) int greedy_chunk(const Rec& r, const Lds& L, int64_t a, int64_t b, bool blank_in, Slot& out, int* ambiguous) {
   Header* h = L.h;
   const int tid = threadIdx.x, NT = blockDim.x;
   const int n = (int)(b - a);
@@ -741,6 +874,11 @@ __device__ int greedy_chunk(const Rec& r, const Lds& L, int64_t a, int64_t b, GL
   bad = __syncthreads_or(bad);
   *ambiguous = 0;
   if (bad) { __syncthreads(); return 0; }
+  const bool at_start = a == 0, at_end = b == r.T;
+  int matches = 0, start = -1, rlast = 0;
+  if (blank_in) {
+    matches = place_literal(L, L.ytok, n, S, blank, at_start, at_end, &start, &rlast);
+  } else {
   // relative walk and token pattern in one scan: low 16 bits r, high 16 bits
   // the running count of token change points
   int carry = 0;
@@ -768,9 +906,7 @@ __device__ int greedy_chunk(const Rec& r, const Lds& L, int64_t a, int64_t b, GL
     __syncthreads();
   }
   const int m = carry >> 16;
-  const int rlast = L.r[n - 1];
-  const bool at_start = a == 0, at_end = b == r.T;
-  int matches = 0, start = -1;
+  rlast = L.r[n - 1];
   if (m == 0) {
     // all-blank chunk: even states, closed form of the placement loop (cu:119-134)
     if (at_start && at_end) { matches = (S == 1) ? 1 : 0; start = 0; }
@@ -830,6 +966,7 @@ __device__ int greedy_chunk(const Rec& r, const Lds& L, int64_t a, int64_t b, GL
     }
     __syncthreads();
   }
+  }
   if (matches != 1) {
     *ambiguous = matches > 1;
     __syncthreads();
@@ -843,39 +980,196 @@ __device__ int greedy_chunk(const Rec& r, const Lds& L, int64_t a, int64_t b, GL
     r.labels[a + f] = L.g[f];
     r.scores[a + f] = L.fs[f];
   }
-  if (tid == 0) {
-    slot->start = start;
-    slot->end = start + rlast;
-    slot->objective = score;
-  }
+  out.start = start;
+  out.end = start + rlast;
+  out.objective = score;
   __syncthreads();
   return 1;
 }
 
 
-// Greedy shortcut of one chunk (at most 128 frames, V <= 32) by wave 0 alone,
-// with no workgroup barrier: lane l owns frames a+l and a+64+l, whose rows are
-// already in registers. Same decisions as greedy_chunk; the pattern scan uses
-// DPP, candidates are compacted with ballots, and the fp32 chunk objective is
-// a readlane chain in frame order. Other waves only wait for the verdict.
-__device__ int greedy_wave(const Rec& r, const Lds& L, int64_t a, int64_t b, uint32_t alpha32,
-                           const float (&row0)[32], const float (&row1)[32], GLB Slot* slot, int* ambiguous) {
+// Reads a descriptor every lane needs: 16-byte vector loads (one request per
+// instruction for the whole wave), then readfirstlane into scalar registers.
+template <class T>
+__device__ inline T load_uniform(const T* x) {
+  static_assert(sizeof(T) % 16 == 0, "16-byte granules");
+  v4i_t tmp[sizeof(T) / 16];
+#pragma unroll
+  for (size_t i = 0; i < sizeof(T) / 16; ++i) tmp[i] = ((const GLB v4i_t*)x)[i];
+  int w[sizeof(T) / 4];
+#pragma unroll
+  for (size_t i = 0; i < sizeof(T) / 4; ++i) w[i] = __builtin_amdgcn_readfirstlane(tmp[i / 4][i % 4]);
+  T out;
+  __builtin_memcpy(&out, w, sizeof(T));
+  return out;
+}
+
+// Substring placement of a chunk's greedy path by wave 0 (blank-free
+// transcripts; cu:119-134). g0 / g1 are the greedy labels of frames lane and
+// lane + 64 (-2 past the chunk). The relative walk r (0 same label, 1 when a
+// blank is involved, 2 token to token) and the token change points form a
+// pattern c_1..c_m; a start state s is a legal placement iff the pattern equals
+// the contiguous target substring y[j .. j+m) (s = 2j+1-r1, r1 = r at the first
+// token), plus the reference's start/end constraints, which for s = 2j+1-r1
+// and terminal s + rlast reduce to an interval of j:
+//   terminal < S        <=>  j <= E,  E = (S - 2 + r1 - rlast) >> 1
+//   b == T: terminal >= S-2  <=>  j >= E
+//   a == 0: s <= 1      <=>  j == 0
+// Candidates come from the three-token keys (eight positions per lane per
+// 16-byte LDS read) and are verified token by token, one per round, until two
+// match. Returns min(number of legal placements, 2), *start and *rlast.
+constexpr int VERIFY_CAP = 16;
+
+__device__ __attribute__((always_inline)) int place_wave(const Lds& L, int g0, int g1, int n, int U, int S, int blank,
+                                                        bool at_start, bool at_end, bool small_vocab, int* start_out,
+                                                        int* rlast_out) {
+  const int lane = threadIdx.x & 63;
+  const int gp0 = wave_shr1_int(g0, -1);
+  const int gp1 = wave_shr1_int(g1, __builtin_amdgcn_readlane(g0, 63));
+  auto step = [&](int f, int g, int gp, int& inc, int& tc) {
+    inc = tc = 0;
+    if (f >= n) return;
+    if (f > 0) inc = g == gp ? 0 : (g == blank || gp == blank ? 1 : 2);  // cu:112-117
+    tc = g != blank && (f == 0 || g != gp);
+  };
+  int inc0, tc0, inc1, tc1;
+  step(lane, g0, gp0, inc0, tc0);
+  step(lane + 64, g1, gp1, inc1, tc1);
+  const int v0 = wave_scan_dpp(inc0 | (tc0 << 16));
+  const int v1 = wave_scan_dpp(inc1 | (tc1 << 16)) + __builtin_amdgcn_readlane(v0, 63);
+  const int m = __builtin_amdgcn_readlane(v1, 63) >> 16;
+  const int rlast = (n <= 64 ? __builtin_amdgcn_readlane(v0, n - 1) : __builtin_amdgcn_readlane(v1, n - 65)) & 0xffff;
+  *rlast_out = rlast;
+  if (m == 0) {  // all-blank chunk: even states, closed form of the placement loop (cu:119-134)
+    *start_out = at_start ? 0 : (at_end ? S - 1 : 0);
+    if (at_start && at_end) return S == 1 ? 1 : 0;
+    if (at_start || at_end) return 1;
+    return min((S + 1) / 2, 2);
+  }
+  // the pattern in LDS for the verification rounds
+  if (tc0) L.pc[(v0 >> 16) - 1] = g0;
+  if (tc1) L.pc[(v1 >> 16) - 1] = g1;
+  // first three pattern tokens and r1 straight from the change-point masks
+  uint64_t m0 = __ballot(tc0), m1 = __ballot(tc1);
+  int c[3] = {0, 0, 0};
+  int r1 = 0;
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    if (m0) {
+      const int l = __builtin_ctzll(m0);
+      m0 &= m0 - 1;
+      c[q] = __builtin_amdgcn_readlane(g0, l);
+      if (q == 0) r1 = __builtin_amdgcn_readlane(v0, l) & 0xffff;
+    } else if (m1) {
+      const int l = __builtin_ctzll(m1);
+      m1 &= m1 - 1;
+      c[q] = __builtin_amdgcn_readlane(g1, l);
+      if (q == 0) r1 = __builtin_amdgcn_readlane(v1, l) & 0xffff;
+    }
+  }
+  const int E = (S - 2 + r1 - rlast) >> 1;
+  const int jlo = at_end ? max(E, 0) : 0;
+  const int jhi = min(min(E, U - m), at_start ? 0 : INT_MAX);
+  int matches = 0, start = -1;
+  if (jlo > jhi) { *start_out = -1; return 0; }
+  const int pc_lo = lane < m ? L.pc[lane] : -3;
+  const int pc_hi = lane + 64 < m ? L.pc[lane + 64] : -3;
+  auto verify = [&](int j) {  // y[j .. j+m) == pattern, all lanes
+    const bool bad = (lane < m && L.ytok[j + lane] != pc_lo) || (lane + 64 < m && L.ytok[j + lane + 64] != pc_hi);
+    return __ballot(bad) == 0;
+  };
+  if (m >= 3 && jhi - jlo >= 8) {
+    const uint32_t pkey = tri_key(c[0], c[1], c[2], small_vocab);
+    // count the key hits first: 8 positions per lane per 16-byte read
+    int total = 0;
+    for (int base = jlo & ~7; base <= jhi; base += 512) {
+      const int j0 = base + 8 * lane;
+      const v4i_t kv = *reinterpret_cast<const v4i_t*>(L.key3 + min(j0, (jhi & ~7)));
+      uint32_t hits = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t key = ((uint32_t)kv[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+        const int j = j0 + e;
+        hits |= (uint32_t)(key == pkey && j >= jlo && j <= jhi) << e;
+      }
+      const int cnt = __builtin_amdgcn_readlane(wave_scan_dpp(__popc(hits)), 63);
+      if (cnt && total + cnt <= VERIFY_CAP) {
+        // verify this block's candidates in order, lowest position first
+        uint64_t lanes_hit = __ballot(hits != 0);
+        while (lanes_hit && matches < 2) {
+          const int l = __builtin_ctzll(lanes_hit);
+          lanes_hit &= lanes_hit - 1;
+          uint32_t h8 = (uint32_t)__builtin_amdgcn_readlane((int)hits, l);
+          while (h8 && matches < 2) {
+            const int j = base + 8 * l + __builtin_ctz(h8);
+            h8 &= h8 - 1;
+            if (verify(j)) {
+              if (matches == 0) start = 2 * j + 1 - r1;
+              ++matches;
+            }
+          }
+        }
+      }
+      total += cnt;
+      if (total > VERIFY_CAP || matches >= 2) break;
+    }
+    if (total <= VERIFY_CAP) {
+      *start_out = start;
+      return matches;
+    }
+    matches = 0;
+    start = -1;
+  } else if (jhi - jlo < 8) {
+    // a few positions (start / end chunks, short transcripts): verify each
+    for (int j = jlo; j <= jhi && matches < 2; ++j) {
+      if (verify(j)) {
+        if (matches == 0) start = 2 * j + 1 - r1;
+        ++matches;
+      }
+    }
+    *start_out = start;
+    return matches;
+  }
+  // many candidates (repetitive transcripts) or m < 3: every position checked
+  // in full by its own lane
+  for (int base = jlo; base <= jhi && matches < 2; base += 64) {  // uniform trip count for the ballots
+    const int j = base + lane;
+    bool hit = j <= jhi;
+    for (int i = 0; i < m && hit; ++i) hit = L.ytok[j + i] == L.pc[i];
+    const uint64_t mask = __ballot(hit);
+    if (mask && start < 0) start = 2 * __builtin_amdgcn_readlane(j, __builtin_ctzll(mask)) + 1 - r1;
+    matches += __popcll(mask);
+  }
+  *start_out = start;
+  return min(matches, 2);
+}
+
+// Greedy shortcut of one chunk (greedy_shortcuts, cu:30-153) for n <= 128
+// frames and V <= 32: lane f of waves 0 and 1 holds frame a+f's row in x.
+// Per frame the unique maximum over the transcript alphabet (cu:65-91):
+// columns outside the alphabet (and past V) read as -inf, so they cannot win
+// and only tie a -inf maximum, which rejects the chunk anyway; IEEE max ignores
+// NaN exactly as the reference's strict '>' scan does, and the maximum is
+// unique iff exactly one column equals it. Wave 0 then places the chunk while
+// wave 1 computes the serial fp32 chunk objective (cu:135-137). Writes the
+// labels and scores of an accepted chunk; *g / *fs return the lane's frame.
+__device__ __attribute__((always_inline)) int greedy_fast(const Lds& L, const float (&x)[32], int n, int U, int S, int V, int blank,
+                           uint32_t alpha32, bool blank_in, bool at_start, bool at_end, Slot& out, int* ambiguous,
+                           int* g_lane, float* fs_lane) {
   Header* h = L.h;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n = (int)(b - a);
-  const int blank = r.blank, S = r.S, U = r.U;
-  int g0 = -2, g1 = -2;
-  float fs0 = 0.0f, fs1 = 0.0f;
-  // Unique maximum over the alphabet columns (cu:65-91). Columns outside the
-  // alphabet (and past V, which hold -inf) read as -inf: they cannot win
-  // and only tie a -inf maximum, which rejects the chunk anyway. A max tree
-  // (IEEE max ignores NaN, as the reference's strict '>' scan does) then
-  // independent equality tests: unique iff exactly one column equals it.
-  // Branch-free, so the two rows of a lane interleave.
-  auto argmax = [&](const float (&row)[32], int f, int& g, float& fs) -> bool {
+  int g = -2;
+  float fs = -0.0f;  // identity of the fp32 sum for padding frames
+  if (tid < 128) {
+    const uint32_t cols = V >= 32 ? 0xffffffffu : ((1u << V) - 1u);
     float v[32];
+    if ((alpha32 & cols) == cols) {
 #pragma unroll
-    for (int c = 0; c < 32; ++c) v[c] = (alpha32 >> c) & 1u ? row[c] : NEG_INF;
+      for (int c = 0; c < 32; ++c) v[c] = x[c];
+    } else {
+#pragma unroll
+      for (int c = 0; c < 32; ++c) v[c] = (alpha32 >> c) & 1u ? x[c] : NEG_INF;
+    }
     float t[16];
 #pragma unroll
     for (int c = 0; c < 16; ++c) t[c] = fmaxf(v[2 * c], v[2 * c + 1]);
@@ -883,140 +1177,52 @@ __device__ int greedy_wave(const Rec& r, const Lds& L, int64_t a, int64_t b, uin
     for (int w = 8; w >= 1; w >>= 1)
 #pragma unroll
       for (int c = 0; c < w; ++c) t[c] = fmaxf(t[2 * c], t[2 * c + 1]);
-    const float m = t[0];
+    const float mx = t[0];
     int count = 0, idx = -1;
 #pragma unroll
     for (int c = 0; c < 32; ++c) {
-      const bool e = v[c] == m;
+      const bool e = v[c] == mx;
       count += e;
       idx = e ? c : idx;
     }
-    const bool live = f < n;
-    g = live ? idx : -2;
-    fs = live ? m : 0.0f;
-    return live && (!isfinite(m) || count != 1);
-  };
-  if (wave == 0) {
-    const bool bad0 = argmax(row0, lane, g0, fs0);
-    const bool bad1 = argmax(row1, lane + 64, g1, fs1);
-    L.fs[lane] = fs0;
-    L.fs[lane + 64] = fs1;
-    if (lane == 0) h->ibuf[5] = __ballot(bad0 || bad1) != 0;
+    const bool live = tid < n;
+    const bool bad = live && (!isfinite(mx) || count != 1);
+    if (live) { g = idx; fs = mx; }
+    L.g[tid] = g;
+    L.fs[tid] = fs;
+    const uint64_t anybad = __ballot(bad);
+    if (lane == 0) h->gbad[wave] = anybad != 0;
   }
+  *g_lane = g;
+  *fs_lane = fs;
   __syncthreads();
   *ambiguous = 0;
-  if (h->ibuf[5]) {  // a tie or a non-finite maximum: no shortcut
+  if (h->gbad[0] | h->gbad[1]) return 0;  // a tie or a non-finite maximum: no shortcut
+  int matches, start, rlast;
+  float score;
+  if (blank_in) {
+    matches = place_literal(L, L.ytok, n, S, blank, at_start, at_end, &start, &rlast);
+    if (tid == 0) h->fbuf[1] = serial_sum128(L.fs);
     __syncthreads();
-    return 0;
-  }
-  if (wave == 1) {
-    // the serial fp32 chunk objective (cu:135-137), overlapped with placement
-    if (lane == 0) h->fbuf[1] = serial_sum(L.fs, n);
-  } else if (wave == 0) {
-    int matches = 0, start = -1, rlast = 0;
-    {
-      // relative walk (cu:112-117) and token change points, packed r | count << 16
-      const int gp0 = wave_shr1_int(g0, -1);
-      const int gp1 = wave_shr1_int(g1, __builtin_amdgcn_readlane(g0, 63));
-      auto step = [&](int f, int g, int gp, int& inc, int& tc) {
-        inc = tc = 0;
-        if (f >= n) return;
-        if (f > 0) inc = g == gp ? 0 : (g == blank || gp == blank ? 1 : 2);
-        tc = g != blank && (f == 0 || g != gp);
-      };
-      int inc0, tc0, inc1, tc1;
-      step(lane, g0, gp0, inc0, tc0);
-      step(lane + 64, g1, gp1, inc1, tc1);
-      const int v0 = wave_scan_dpp(inc0 | (tc0 << 16));
-      const int v1 = wave_scan_dpp(inc1 | (tc1 << 16)) + __builtin_amdgcn_readlane(v0, 63);
-      const int m = __builtin_amdgcn_readlane(v1, 63) >> 16;
-      rlast = (n <= 64 ? __builtin_amdgcn_readlane(v0, n - 1) : __builtin_amdgcn_readlane(v1, n - 65)) & 0xffff;
-      if (tc0) { L.pc[(v0 >> 16) - 1] = g0; L.pd[(v0 >> 16) - 1] = v0 & 0xffff; }
-      if (tc1) { L.pc[(v1 >> 16) - 1] = g1; L.pd[(v1 >> 16) - 1] = v1 & 0xffff; }
-      const bool at_start = a == 0, at_end = b == r.T;
-      if (m == 0) {  // all-blank chunk: closed form of the placement loop (cu:119-134)
-        if (at_start && at_end) { matches = (S == 1) ? 1 : 0; start = 0; }
-        else if (at_start) { matches = 1; start = 0; }
-        else if (at_end) { matches = 1; start = S - 1; }
-        else { matches = (S + 1) / 2; start = 0; }
-      } else {
-        const int r1 = L.pd[0];
-        const int pre = min(m, 3);
-        const int c1 = L.pc[0], c2 = pre > 1 ? L.pc[1] : 0, c3 = pre > 2 ? L.pc[2] : 0;
-        auto placeable = [&](int j) {  // cu:119-123 for target position j (state 2j+1-r1)
-          const int s = 2 * j + 1 - r1;
-          const int terminal = s + rlast;
-          return !((at_start && s > 1) || terminal >= S || (at_end && terminal < S - 2));
-        };
-        int count = 0;
-        for (int base = 0; base + m <= U; base += 256) {  // 4 x 64 positions per round of LDS reads
-          int t0[4], t1[4], t2[4];
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {  // clamped: reads at most ytok[U + 2], in the sentinel padding
-            const int j = min(base + 64 * u + lane, U);
-            t0[u] = L.ytok[j];
-            t1[u] = L.ytok[j + 1];
-            t2[u] = L.ytok[j + 2];
-          }
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int j = base + 64 * u + lane;
-            const bool hit = (j + m <= U) & (t0[u] == c1) & ((pre < 2) | (t1[u] == c2)) & ((pre < 3) | (t2[u] == c3)) &
-                             placeable(j);
-            const uint64_t mask = __ballot(hit);
-            if (hit) {
-              const int k = count + (int)lanes_below(mask);
-              if (k < CAND_CAP) { L.cand[k] = j; L.candok[k] = 1; }
-            }
-            count += __popcll(mask);
-          }
-        }
-        if (count <= CAND_CAP) {
-          const int width = m - pre;
-          for (int q = lane; q < count * width; q += 64) {
-            const int ci = q / width, i = pre + q % width;
-            if (L.ytok[L.cand[ci] + i] != L.pc[i]) L.candok[ci] = 0;
-          }
-          for (int base = 0; base < count; base += 64) {
-            const int ci = base + lane;
-            const bool ok = ci < count && L.candok[ci];
-            const uint64_t mask = __ballot(ok);
-            if (mask && start < 0)
-              start = 2 * __builtin_amdgcn_readlane(ci < count ? L.cand[ci] : 0, __builtin_ctzll(mask)) + 1 - r1;
-            matches += __popcll(mask);
-          }
-        } else {
-          // more prefiltered candidates than the list holds: exact scan
-          for (int base = 0; base + m <= U; base += 64) {  // uniform trip count for the ballots
-            const int j = base + lane;
-            bool hit = j + m <= U && placeable(j);
-            for (int i = 0; i < m && hit; ++i) hit = L.ytok[j + i] == L.pc[i];
-            const uint64_t mask = __ballot(hit);
-            if (mask && start < 0) start = 2 * __builtin_amdgcn_readlane(j, __builtin_ctzll(mask)) + 1 - r1;
-            matches += __popcll(mask);
-          }
-        }
-      }
+    score = h->fbuf[1];
+  } else {
+    if (wave == 0) {
+      const int m = place_wave(L, L.g[lane], L.g[lane + 64], n, U, S, blank, at_start, at_end, V <= 32, &start, &rlast);
+      if (lane == 0) { h->ibuf[3] = m; h->ibuf[4] = start; h->ibuf[6] = rlast; }
+    } else if (wave == 1 && lane == 0) {
+      h->fbuf[1] = serial_sum128(L.fs);  // padding frames add -0.0, an exact identity
     }
-    if (lane == 0) { h->ibuf[3] = matches; h->ibuf[4] = start; h->ibuf[6] = rlast; }
+    __syncthreads();
+    matches = h->ibuf[3];
+    start = h->ibuf[4];
+    rlast = h->ibuf[6];
+    score = h->fbuf[1];
   }
-  __syncthreads();
-  const int matches = h->ibuf[3];
-  const int start = h->ibuf[4];
-  const int rlast = h->ibuf[6];
-  const float score = h->fbuf[1];
-  __syncthreads();
   *ambiguous = matches > 1;
   if (matches != 1 || !isfinite(score)) return 0;  // cu:129-139
-  if (wave == 0) {  // finish's label/score gather collapses to g and fs here
-    if (lane < n) { r.labels[a + lane] = g0; r.scores[a + lane] = fs0; }
-    if (lane + 64 < n) { r.labels[a + lane + 64] = g1; r.scores[a + lane + 64] = fs1; }
-    if (lane == 0) {
-      slot->start = start;
-      slot->end = start + rlast;
-      slot->objective = score;
-    }
-  }
+  out.start = start;
+  out.end = start + rlast;
+  out.objective = score;
   return 1;
 }
 
@@ -1053,77 +1259,6 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) conventional_kernel(Param
 __device__ inline int xcd_slot(int bid, int total) {
   const int per = (total + 7) / 8;
   return (bid % 8) * per + bid / 8;
-}
-
-// Optimized mode, one workgroup per 128-frame chunk: greedy shortcut, else
-// relaxed chunk DP (cu:721-726). Writes the chunk's labels/scores and its slot.
-template <int K, int D>
-__global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
-  extern __shared__ __align__(16) unsigned char lds_raw[];
-  const Lds L = carve(lds_raw, p);
-  const int slot_index = xcd_slot(blockIdx.x, p.total_slots);
-  if (slot_index >= p.total_slots) return;
-  const SlotEntry se = load_pod(glb(p.slot_entries) + slot_index);
-  const int rec = se.record;
-  const int chunk = se.chunk;
-  const RecordDesc d = load_pod(glb(p.desc) + rec);
-  const Rec r = make_rec(d, p, L);
-  const int64_t a = (int64_t)chunk * p.H;
-  const int64_t b = min(r.T, a + p.H);
-  const int n = (int)(b - a);
-  const int tid = threadIdx.x;
-  // Issue the chunk's emission rows first so their latency overlaps target
-  // staging: for V <= 32, lane l of wave 0 loads rows a+l and a+64+l.
-  const bool fast = p.mode == 2 && d.vocab <= 32 && (d.vocab & 3) == 0 &&
-                    (reinterpret_cast<uintptr_t>(se.rows) & 15) == 0 && n <= 128;
-  float row0[32], row1[32];
-#pragma unroll
-  for (int c = 0; c < 32; ++c) { row0[c] = NEG_INF; row1[c] = NEG_INF; }
-  if (fast && tid < 64) {
-    auto load_row = [&](int f, float (&row)[32]) {
-      const GLB v4f_t* src = (const GLB v4f_t*)(glb(se.rows) + f * (int64_t)d.vocab);
-#pragma unroll
-      for (int q = 0; q < 8; ++q)
-        if (4 * q < d.vocab) {
-          const v4f_t v = src[q];
-          row[4 * q] = v.x; row[4 * q + 1] = v.y; row[4 * q + 2] = v.z; row[4 * q + 3] = v.w;
-        }
-    };
-    if (tid < n) load_row(tid, row0);
-    if (tid + 64 < n) load_row(tid + 64, row1);
-  }
-  const Staged st = stage_tokens(d, p, rec, L, p.mode != 2 ? ALPHABET_NONE : (fast ? ALPHABET_MASK32 : ALPHABET_BITMAP));
-  GLB Slot* slot = glb(p.slots) + slot_index;
-  if (st.status >= 2) {  // rejected before any label-indexed read (cu:36, cu:642-652)
-    write_failed(r, a, b);
-    if (tid == 0) {
-      Slot s{};
-      s.a = (int)a; s.b = (int)b; s.objective = NEG_INF; s.status = (int16_t)st.status;
-      store_pod(slot, s);
-    }
-    return;
-  }
-  int accepted = 0, ambiguous = 0;
-  if (p.mode == 2)
-    accepted = fast ? greedy_wave(r, L, a, b, st.alpha32, row0, row1, slot, &ambiguous)
-                    : greedy_chunk(r, L, a, b, slot, &ambiguous);
-  if (!accepted) {  // initial chunk DP (cu:721-726), relaxed init for a > 0
-    GLB float* fr = r.frontier ? r.frontier + (int64_t)chunk * r.S : nullptr;
-    const DPOut o = dp_interval<K, D>(r, L, a, b, b == r.T, nullptr, a + 1, fr, TRACE_ALWAYS);
-    if (tid == 0) {
-      slot->objective = o.score;
-      slot->end = o.terminal;
-      slot->start = o.start;
-    }
-  }
-  if (tid == 0) {
-    slot->a = (int)a;
-    slot->b = (int)b;
-    slot->flag = 1;
-    slot->kind = (int16_t)(accepted ? 1 : (ambiguous ? 2 : 0));
-    slot->status = 0;
-    slot->frontier_end = (!accepted && r.frontier) ? (int)b : 0;
-  }
 }
 
 // Optimized mode, one workgroup per record, after the chunk kernel: repair
@@ -1370,18 +1505,175 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
   }
 }
 
+// Optimized mode, one workgroup per chunk of H frames (XCD-aware order): it
+// stages and validates the record's targets, takes the greedy shortcut
+// (cu:30-153) or runs the relaxed chunk DP (cu:721-726), and writes the
+// chunk's labels, scores and slot.
+template <int K, int D>
+__global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  const Lds L = carve(lds_raw, p);
+  const int tid = threadIdx.x;
+  const int slot_index = xcd_slot(blockIdx.x, p.total_slots);
+  if (slot_index >= p.total_slots) return;
+  const ChunkDesc c = load_uniform(p.chunks + slot_index);
+  const int64_t a = (int64_t)c.chunk * p.H;
+  const int64_t b = a + c.n;
+  const int n = c.n;
+  const bool fast = (c.flags & CHUNK_FAST) != 0;
+  // The chunk's rows first, so their latency overlaps target staging: lane f
+  // of waves 0-1 loads row a+f (V <= 32, 16-byte aligned).
+  float x[32];
+#pragma unroll
+  for (int q = 0; q < 32; ++q) x[q] = NEG_INF;
+  if (fast && tid < n) {
+    const GLB v4f_t* src = (const GLB v4f_t*)(glb(c.rows) + (int64_t)tid * c.vocab);
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (4 * q < c.vocab) {
+        const v4f_t v = src[q];
+        x[4 * q] = v.x; x[4 * q + 1] = v.y; x[4 * q + 2] = v.z; x[4 * q + 3] = v.w;
+      }
+  }
+  const Staged st = stage_targets(glb(c.targets), c.tokens, c.vocab, c.blank, c.frames, c.record, p, L,
+                                  p.mode != 2 ? ALPHABET_NONE : (fast ? ALPHABET_MASK32 : ALPHABET_BITMAP), fast);
+  Slot out{};
+  out.a = (int)a;
+  out.b = (int)b;
+  out.flag = 1;
+  out.objective = NEG_INF;
+  GLB int64_t* labels = glb(p.labels) + c.out;
+  GLB float* scores = glb(p.scores) + c.out;
+  if (st.status >= 2) {  // rejected before any label-indexed read (cu:36, cu:642-652)
+    for (int f = tid; f < n; f += blockDim.x) { labels[f] = -1; scores[f] = NEG_INF; }
+    out.flag = 0;
+    out.status = (int16_t)st.status;
+  } else {
+    int accepted = 0, ambiguous = 0;
+    if (p.mode == 2 && fast) {
+      int g;
+      float fs;
+      accepted = greedy_fast(L, x, n, c.tokens, 2 * c.tokens + 1, c.vocab, c.blank, st.alpha32, st.blank_in,
+                             a == 0, b == c.frames, out, &ambiguous, &g, &fs);
+      if (accepted && tid < n) {  // finish's label/score gather collapses to g and fs (cu:642-667)
+        labels[tid] = g;
+        scores[tid] = fs;
+      }
+    }
+    if (!accepted) {
+      const RecordDesc d = load_uniform(p.desc + c.record);
+      const Rec r = make_rec(d, p, L);
+      if (p.mode == 2 && !fast) accepted = greedy_chunk(r, L, a, b, st.blank_in, out, &ambiguous);
+      if (!accepted) {  // initial chunk DP (cu:721-726), relaxed init for a > 0
+        GLB float* fr = r.frontier ? r.frontier + (int64_t)c.chunk * r.S : nullptr;
+        const DPOut o = dp_interval<K, D>(r, L, a, b, b == r.T, nullptr, a + 1, fr, TRACE_ALWAYS);
+        out.objective = o.score;
+        out.end = o.terminal;
+        out.start = o.start;
+        out.frontier_end = r.frontier ? (int)b : 0;
+      }
+    }
+    out.kind = (int16_t)(accepted ? 1 : (ambiguous ? 2 : 0));
+  }
+  if (tid == 0) store_pod(glb(p.slots) + slot_index, out);
+}
+
+// Label of state s read straight from the int64 targets (tail fast path).
+__device__ inline int label_at(const GLB int64_t* y, int blank, int s) { return (s & 1) ? (int)y[s >> 1] : blank; }
+
+// Optimized mode, one workgroup per record, after the chunk kernel: repair
+// rounds, seam validation, full-DP fallback, final path and every per-record
+// output (plan_repairs cu:164-228, repair DP cu:727-760, validate_seams
+// cu:562-592, fallback_recurrence cu:552-559, finish cu:642-667).
+//
+// Fast path (at most 64 chunks): when every chunk objective is finite and
+// every seam is legal, the repair rounds merge nothing (plan_repairs joins
+// every neighbour and its budget preflight proposes no region) and
+// validate_seams stitches iff the fp32 total is finite. Wave 0 checks all
+// seams at once from registers and writes the record's outputs.
 template <int K, int D>
 __global__ void __launch_bounds__(K == 32 ? 640 : 256) tail_kernel(Params p) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   const Lds L = carve(lds_raw, p);
+  Header* h = L.h;
+  const int tid = threadIdx.x;
   const int rec = blockIdx.x;
-  const RecordDesc d = load_pod(glb(p.desc) + rec);
-  const Rec r = make_rec(d, p, L);
-  const int n = (int)(1 + (r.T - 1) / p.H);
+  const RecordDesc d = load_uniform(p.desc + rec);
+  const int n = (int)(1 + (d.frames - 1) / p.H);
   GLB Slot* gs = glb(p.slots) + d.chunk_offset;
+  if (n <= 64) {
+    if (tid < 64) {
+      const int k = tid;
+      const bool valid = k < n;
+      const Slot sk = load_pod(gs + (valid ? k : 0));
+      const int status0 = __builtin_amdgcn_readfirstlane(sk.status);
+      const int S = 2 * d.tokens + 1;
+      const bool frontier_on = d.frontier_offset >= 0;
+      int done = 0;
+      if (status0 >= 2) {  // rejected record: every chunk wrote -1 / -inf
+        done = 1;
+        if (k == 0) {
+          glb(p.status)[rec] = status0;
+          glb(p.objective)[rec] = NEG_INF;
+          glb(p.stitched)[rec] = 0;
+          glb(p.repair_passes)[rec] = 0;
+          glb(p.repaired_frames)[rec] = 0;
+          for (int q = 0; q < 3; ++q) { glb(p.shortcut_stats)[3 * rec + q] = 0; glb(p.routing_stats)[3 * rec + q] = 0; }
+          if (p.reuse_stats)
+            for (int q = 0; q < 4; ++q) glb(p.reuse_stats)[4 * rec + q] = 0;
+        }
+      } else {
+        const int end_prev = wave_shr1_int(sk.end, 0);
+        bool ok = !valid || isfinite(sk.objective);
+        if (valid && k > 0) {  // legal_seam, cu:157-161
+          const int jump = sk.start - end_prev;
+          bool seam = jump == 0 || jump == 1;
+          if (jump == 2) {
+            const GLB int64_t* y = glb(d.targets);
+            const int ls = label_at(y, d.blank, sk.start);
+            seam = ls != d.blank && ls != label_at(y, d.blank, sk.start - 2);
+          }
+          ok = ok && seam;
+        }
+        if (__ballot(!ok) == 0) {
+          float total = 0.0f;  // cu:578-584: chunk objectives summed in chunk order
+          for (int i = 0; i < n; ++i) total += readlane_f(sk.objective, i);
+          if (isfinite(total)) {
+            done = 1;
+            const uint64_t shortcut = __ballot(valid && sk.kind == 1);
+            const uint64_t amb = __ballot(valid && sk.kind == 2);
+            const uint64_t dp = __ballot(valid && sk.kind != 1);
+            int frames = valid && sk.kind == 1 ? sk.b - sk.a : 0;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) frames += __shfl_xor(frames, off, 64);
+            if (k == 0) {
+              glb(p.status)[rec] = 0;
+              glb(p.objective)[rec] = total;
+              glb(p.stitched)[rec] = 1;
+              glb(p.repair_passes)[rec] = 0;
+              glb(p.repaired_frames)[rec] = 0;
+              glb(p.shortcut_stats)[3 * rec + 0] = __popcll(shortcut);
+              glb(p.shortcut_stats)[3 * rec + 1] = frames;
+              glb(p.shortcut_stats)[3 * rec + 2] = __popcll(amb);
+              for (int q = 0; q < 3; ++q) glb(p.routing_stats)[3 * rec + q] = 0;
+              if (p.reuse_stats) {
+                GLB int64_t* u = glb(p.reuse_stats) + 4 * rec;
+                u[0] = 0; u[1] = 0; u[2] = frontier_on ? (int64_t)__popcll(dp) * S : 0; u[3] = 0;
+              }
+            }
+          }
+        }
+      }
+      if (tid == 0) h->last = done;
+    }
+    __syncthreads();
+    if (h->last) return;
+    __syncthreads();
+  }
+  const Rec r = make_rec(d, p, L);
   if (n <= p.lds_tail_slots) {
     Slot* ls = reinterpret_cast<Slot*>(lds_raw + ((uintptr_t)L.tslots - (uintptr_t)lds_raw));
-    for (int c = threadIdx.x; c < n; c += blockDim.x) ls[c] = load_pod(gs + c);
+    for (int k = tid; k < n; k += blockDim.x) ls[k] = load_pod(gs + k);
     __syncthreads();
     tail_body<K, D>(p, d, rec, r, L, ls, true);
   } else {
@@ -1443,14 +1735,14 @@ template <int K, int D>
 int launch_geometry(const ffa::Params& p, int NT, size_t lds, bool optimized, hipStream_t stream) {
   hipEvent_t start = g_profile_start, stop = g_profile_stop;
   g_profile_start = g_profile_stop = nullptr;
-  if (start) hipEventRecord(start, stream);
+  if (start) (void)hipEventRecord(start, stream);
   if (!optimized) {
     hipLaunchKernelGGL((ffa::conventional_kernel<K, D>), dim3(p.count), dim3(NT), lds, stream, p);
   } else {
     const int grid = 8 * ((p.total_slots + 7) / 8);
     hipLaunchKernelGGL((ffa::chunk_kernel<K, D>), dim3(grid), dim3(std::max(NT, 128)), lds, stream, p);
   }
-  if (stop) hipEventRecord(stop, stream);
+  if (stop) (void)hipEventRecord(stop, stream);
   if (optimized) hipLaunchKernelGGL((ffa::tail_kernel<K, D>), dim3(p.count), dim3(NT), lds, stream, p);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(FFA_E_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
@@ -1565,9 +1857,10 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
   geometry(s_max, &K, &NT);
   const int64_t v_words = (v_max + 31) / 32;
   const int64_t tail_slots = optimized ? std::min<int64_t>(n_max, ffa::TAIL_SLOT_CAP) : 0;
-  const int64_t greedy_bytes = 20 * align_up(H, 32) + 2048 + align_up(2 * d_cap, 16) + 8 * v_words;
+  const int64_t greedy_bytes = 20 * ffa::greedy_frames(H) + 2048 + align_up(2 * d_cap, 16) + 8 * v_words;
   const int64_t region = std::max(greedy_bytes, 32 * tail_slots);
-  const int64_t lds = align_up((int64_t)sizeof(ffa::Header), 16) + align_up(2 * (std::max<int64_t>(u_max, 1) + ffa::YTOK_PAD), 16) + region;
+  const int64_t targets = align_up(2 * (std::max<int64_t>(u_max, 1) + ffa::YTOK_PAD), 16);
+  const int64_t lds = align_up((int64_t)sizeof(ffa::Header), 16) + 2 * targets + region;
   if (lds > 64 * 1024) return fail(FFA_E_INVALID, "batch needs more than 64 KiB of LDS per workgroup");
   int64_t ws = align_up(4 * bp_words, 256);
   const int64_t ws_slots = ws;
@@ -1577,7 +1870,7 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
   std::memset(plan, 0, sizeof(*plan));
   plan->count = count;
   plan->total_frames = total_frames;
-  plan->table_bytes = count * (int64_t)sizeof(ffa::RecordDesc) + (int64_t)sizeof(ffa::SlotEntry) * slots;
+  plan->table_bytes = count * (int64_t)sizeof(ffa::RecordDesc) + (int64_t)sizeof(ffa::ChunkDesc) * slots;
   plan->workspace_bytes = std::max<int64_t>(ws, 256);
   plan->reuse_rows = frontier ? count : 0;
   int64_t* in = plan->internal;
@@ -1610,7 +1903,7 @@ int ffa_align_describe(const ffa_align_plan* plan, const ffa_record* records, vo
   const bool frontier = in[I_FRONTIER] != 0;
   const int64_t H = in[I_H];
   auto* desc = static_cast<ffa::RecordDesc*>(host_table);
-  auto* entries = reinterpret_cast<ffa::SlotEntry*>(desc + count);
+  auto* chunks = reinterpret_cast<ffa::ChunkDesc*>(desc + count);
   int64_t frame = 0, bp = 0, fr = 0;
   int32_t slot = 0;
   for (int64_t i = 0; i < count; ++i) {
@@ -1632,16 +1925,32 @@ int ffa_align_describe(const ffa_align_plan* plan, const ffa_record* records, vo
       d.frontier_offset = fr;
       fr += n * S;
     }
-    frame += r.frames;
-    bp += r.frames * stride_of(S);
     if (optimized) {
+      // greedy fast path: whole rows in registers (V <= 32, 16-byte rows) and
+      // one frame per lane of two waves
+      const bool fast = in[I_MODE] == 2 && H <= 128 && r.vocab <= 32 && r.vocab % 4 == 0 &&
+                        (reinterpret_cast<uintptr_t>(r.emissions) & 15) == 0;
       for (int64_t c = 0; c < n; ++c) {
-        entries[slot + c].rows = r.emissions + c * H * r.vocab;
-        entries[slot + c].record = (int32_t)i;
-        entries[slot + c].chunk = (int32_t)c;
+        ffa::ChunkDesc& e = chunks[slot + c];
+        std::memset(&e, 0, sizeof(e));
+        e.rows = r.emissions + c * H * r.vocab;
+        e.targets = r.targets;
+        e.out = frame + c * H;
+        e.frames = (int32_t)r.frames;
+        e.tokens = (int32_t)r.tokens;
+        e.vocab = (int32_t)r.vocab;
+        e.blank = (int32_t)r.blank;
+        e.record = (int32_t)i;
+        e.chunk = (int32_t)c;
+        e.n = (int32_t)std::min<int64_t>(H, r.frames - c * H);
+        e.flags = fast ? ffa::CHUNK_FAST : 0;
+        e.nchunks = (int32_t)n;
+        e.first_slot = slot;
       }
       slot += (int32_t)n;
     }
+    frame += r.frames;
+    bp += r.frames * stride_of(S);
   }
   return FFA_OK;
 }
@@ -1660,7 +1969,7 @@ extern "C" int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_opti
   if (o->mode != in[I_MODE] || o->chunk_frames != in[I_H]) return fail(FFA_E_INVALID, "options differ from the plan");
   ffa::Params p{};
   p.desc = static_cast<const ffa::RecordDesc*>(device_table);
-  p.slot_entries = reinterpret_cast<const ffa::SlotEntry*>(p.desc + plan->count);
+  p.chunks = reinterpret_cast<const ffa::ChunkDesc*>(p.desc + plan->count);
   p.validity = emission_validity;
   p.labels = out->labels;
   p.scores = out->scores;

@@ -124,6 +124,35 @@ def test_unchecked_inputs_and_mask():
         compare(es, ys, mode=mode, validity=[True, False, True], where="mask")
 
 
+def test_blank_inside_targets_unchecked():
+    """Targets holding the blank id (accepted only with check_inputs=False). The
+    greedy placement must follow the reference's literal state loop
+    (alignment.cu:119-134): a blank target sits at an odd state, so e.g. an
+    all-blank first chunk has two legal starts (0 and 1) and is ambiguous.
+    Covers the two-wave fast path (V=32) and the general path (V=40, V=6)."""
+    rng = np.random.default_rng(77)
+    es, ys = [], []
+    for i in range(18):
+        V = (32, 40, 6)[i % 3]
+        U = int(rng.integers(2, 40))
+        y = rng.integers(1, V, size=U).astype(np.int64)
+        y[rng.random(U) < 0.3] = 0
+        if i % 6 == 0:
+            y[0] = 0  # transcript starts with the blank: all-blank opening chunk
+        T = int(rng.integers(2 * U + 2, 420))
+        es.append(workloads.peaky(rng, y, T, V, 0))
+        ys.append(y)
+    print("blank inside targets", flush=True)
+    for mode in ("optimized", "conventional"):
+        compare(es, ys, mode=mode, check_inputs=False, where="blank-in-targets")
+    # a hand-built case: targets [0, 5], the first 130 frames peaky on the blank
+    e = np.full((300, 32), -9.0, dtype=np.float32)
+    e[:200, 0] = 0.0
+    e[200:, 5] = 0.0
+    got = compare([e], [np.array([0, 5])], mode="optimized", check_inputs=False, where="[0,5]")
+    assert got["shortcut_stats"][0, 2] >= 1  # the all-blank opening chunk is ambiguous
+
+
 def test_c_abi_direct_call():
     """Drive the HIP library through its C entry points (ctypes), with caller-
     allocated device buffers, and compare with the oracle."""
