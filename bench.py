@@ -100,6 +100,9 @@ def main() -> int:
     parser.add_argument("--mode", default="optimized", choices=["optimized", "conventional"])
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     parser.add_argument("--no-conventional", action="store_true", help="skip the conventional-mode figures")
+    parser.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                        help="after the timed work, run 10 plain device copies of MIB MiB (a known-size "
+                             "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE counter passes)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: the alignment path has no multi-GPU mode in this build "
@@ -163,6 +166,13 @@ def main() -> int:
                                 "dp_cells_per_s": batch.cells / c_step, "kernel_us": c_kernel_ms * 1e3,
                                 "roofline_frac": c_achieved / HBM_PEAK_GBS}
     line["cpu_baseline"] = None if args.no_cpu else cpu_baseline(batch)
+    if args.calibrate_copy > 0:
+        src = torch.ones(args.calibrate_copy << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        line["calibration_copy_bytes"] = src.numel() * 4
     print(json.dumps(line), flush=True)
     return 0
 

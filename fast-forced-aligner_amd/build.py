@@ -4,7 +4,8 @@ Produces, inside ``fast_forced_aligner/``:
   * ``libffa_hip.so``  - the HIP kernels and the C ABI of ``include/ffa.h``
     (hipcc, gfx950 only);
   * ``_ffa_torch.so``  - the PyTorch operators ``fast_forced_aligner_cuda::align``
-    and ``::emission_validity`` on top of that ABI (g++ against torch's headers).
+    and ``::emission_validity`` on top of that ABI, plus the Python module
+    ``_ffa_torch`` whose ``align`` the package calls (g++ against torch's headers).
 
 Run ``python fast-forced-aligner_amd/build.py`` (or ``__graft_entry__.build()``).
 hipcc cross-compiles for gfx950 without a GPU.
@@ -58,14 +59,16 @@ def build_torch(verbose: bool = False) -> Path:
     target = OUT / "_ffa_torch.so"
     tmp = target.with_suffix(".so.tmp")
     abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
-    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-w",
+    import sysconfig
+
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-w", "-fvisibility=hidden",
            f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
-           f"-I{INCLUDE}", f"-I{ROCM / 'include'}"]
+           f"-I{INCLUDE}", f"-I{ROCM / 'include'}", f"-I{sysconfig.get_paths()['include']}"]
     cmd += [f"-I{p}" for p in cpp_extension.include_paths()]
     cmd += [str(CSRC / "ffa_torch.cpp"), "-o", str(tmp), f"-L{OUT}", "-lffa_hip"]
     for lib_dir in cpp_extension.library_paths():
         cmd += [f"-L{lib_dir}"]
-    cmd += ["-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch_hip", "-Wl,-rpath,$ORIGIN"]
+    cmd += ["-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch_hip", "-ltorch_python", "-Wl,-rpath,$ORIGIN"]
     _run(cmd, verbose)
     os.replace(tmp, target)
     return target

@@ -62,26 +62,28 @@ struct Slot {  // per-chunk state of optimized mode (cu:1021-1029 buffers), 32 b
   int16_t flag;    // merged-interval flag of the repair rounds
   int16_t kind;    // 0 chunk DP, 1 greedy shortcut, 2 chunk DP after an ambiguous placement
   int16_t status;  // record status seen by the chunk (>= 2: rejected)
-  int16_t reserved;
+  int16_t skip_ok; // l[start] != blank && l[start] != l[start-2]: a +2 seam into start is legal
 };
 static_assert(sizeof(Slot) == 32, "slot layout");
 
-// Per-chunk descriptor of optimized mode: everything the greedy fast path
-// needs, so a workgroup starts with one scalar load and no dependent lookups.
-struct ChunkDesc {
-  const float* rows;        // first emission row of the chunk
-  const int64_t* targets;   // the record's targets
-  int64_t out;              // index of the chunk's first frame in labels / scores
-  int32_t frames, tokens, vocab, blank;  // T, U, V, blank of the record
-  int32_t record, chunk, n, flags;       // n = frames in this chunk; flags: CHUNK_*
-  int32_t nchunks, first_slot;           // the record's chunk count and first slot
+// Per-chunk table entry of optimized mode, 16 bytes so that a whole batch's
+// table usually stays small enough for the runtime's in-queue copy. It holds
+// what the row loads need, so they are issued before the record descriptor
+// arrives:
+//   word bits 0-15 record, 16-24 frames in the chunk - 1, 25-27 V/4 - 1 and
+//   bit 31 the greedy fast path (V <= 32, V % 4 == 0, 16-byte aligned rows,
+//   at most 128 frames, greedy shortcuts on).
+struct ChunkEntry {
+  const float* rows;  // first emission row of the chunk
+  uint32_t word;
+  int32_t chunk;
 };
-static_assert(sizeof(ChunkDesc) == 64, "chunk descriptor layout");
-enum { CHUNK_FAST = 1 };  // V <= 32, V % 4 == 0, 16-byte aligned rows, n <= 128, greedy on
+static_assert(sizeof(ChunkEntry) == 16, "chunk entry layout");
+constexpr uint32_t CHUNK_FAST = 1u << 31;
 
 struct Params {
   const RecordDesc* desc;
-  const ChunkDesc* chunks;
+  const ChunkEntry* chunks;
   const uint8_t* validity;
   int64_t* labels;
   float* scores;
@@ -1516,34 +1518,37 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
   const int tid = threadIdx.x;
   const int slot_index = xcd_slot(blockIdx.x, p.total_slots);
   if (slot_index >= p.total_slots) return;
-  const ChunkDesc c = load_uniform(p.chunks + slot_index);
-  const int64_t a = (int64_t)c.chunk * p.H;
-  const int64_t b = a + c.n;
-  const int n = c.n;
-  const bool fast = (c.flags & CHUNK_FAST) != 0;
-  // The chunk's rows first, so their latency overlaps target staging: lane f
-  // of waves 0-1 loads row a+f (V <= 32, 16-byte aligned).
+  const ChunkEntry ce = load_uniform(p.chunks + slot_index);
+  const int rec = (int)(ce.word & 0xffffu);
+  const int n = (int)((ce.word >> 16) & 0x1ffu) + 1;
+  const bool fast = (ce.word & CHUNK_FAST) != 0;
+  const int64_t a = (int64_t)ce.chunk * p.H;
+  const int64_t b = a + n;
+  // The chunk's rows first, so their latency overlaps the record descriptor
+  // and target staging: lane f of waves 0-1 loads row a+f (fast path only).
   float x[32];
 #pragma unroll
   for (int q = 0; q < 32; ++q) x[q] = NEG_INF;
   if (fast && tid < n) {
-    const GLB v4f_t* src = (const GLB v4f_t*)(glb(c.rows) + (int64_t)tid * c.vocab);
+    const int quads = (int)((ce.word >> 25) & 7u) + 1;  // V / 4
+    const GLB v4f_t* src = (const GLB v4f_t*)glb(ce.rows) + (int64_t)tid * quads;
 #pragma unroll
     for (int q = 0; q < 8; ++q)
-      if (4 * q < c.vocab) {
+      if (q < quads) {
         const v4f_t v = src[q];
         x[4 * q] = v.x; x[4 * q + 1] = v.y; x[4 * q + 2] = v.z; x[4 * q + 3] = v.w;
       }
   }
-  const Staged st = stage_targets(glb(c.targets), c.tokens, c.vocab, c.blank, c.frames, c.record, p, L,
+  const RecordDesc d = load_uniform(p.desc + rec);
+  const Staged st = stage_targets(glb(d.targets), d.tokens, d.vocab, d.blank, d.frames, rec, p, L,
                                   p.mode != 2 ? ALPHABET_NONE : (fast ? ALPHABET_MASK32 : ALPHABET_BITMAP), fast);
   Slot out{};
   out.a = (int)a;
   out.b = (int)b;
   out.flag = 1;
   out.objective = NEG_INF;
-  GLB int64_t* labels = glb(p.labels) + c.out;
-  GLB float* scores = glb(p.scores) + c.out;
+  GLB int64_t* labels = glb(p.labels) + d.frame_offset + a;
+  GLB float* scores = glb(p.scores) + d.frame_offset + a;
   if (st.status >= 2) {  // rejected before any label-indexed read (cu:36, cu:642-652)
     for (int f = tid; f < n; f += blockDim.x) { labels[f] = -1; scores[f] = NEG_INF; }
     out.flag = 0;
@@ -1553,19 +1558,18 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
     if (p.mode == 2 && fast) {
       int g;
       float fs;
-      accepted = greedy_fast(L, x, n, c.tokens, 2 * c.tokens + 1, c.vocab, c.blank, st.alpha32, st.blank_in,
-                             a == 0, b == c.frames, out, &ambiguous, &g, &fs);
+      accepted = greedy_fast(L, x, n, d.tokens, 2 * d.tokens + 1, d.vocab, d.blank, st.alpha32, st.blank_in,
+                             a == 0, b == d.frames, out, &ambiguous, &g, &fs);
       if (accepted && tid < n) {  // finish's label/score gather collapses to g and fs (cu:642-667)
         labels[tid] = g;
         scores[tid] = fs;
       }
     }
     if (!accepted) {
-      const RecordDesc d = load_uniform(p.desc + c.record);
       const Rec r = make_rec(d, p, L);
       if (p.mode == 2 && !fast) accepted = greedy_chunk(r, L, a, b, st.blank_in, out, &ambiguous);
       if (!accepted) {  // initial chunk DP (cu:721-726), relaxed init for a > 0
-        GLB float* fr = r.frontier ? r.frontier + (int64_t)c.chunk * r.S : nullptr;
+        GLB float* fr = r.frontier ? r.frontier + (int64_t)ce.chunk * r.S : nullptr;
         const DPOut o = dp_interval<K, D>(r, L, a, b, b == r.T, nullptr, a + 1, fr, TRACE_ALWAYS);
         out.objective = o.score;
         out.end = o.terminal;
@@ -1574,12 +1578,15 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
       }
     }
     out.kind = (int16_t)(accepted ? 1 : (ambiguous ? 2 : 0));
+    const int s0 = out.start;  // skip rule at the chunk's start state (cu:157-161), for the tail's seam check
+    if (s0 >= 2) {
+      const int l0 = (s0 & 1) ? (int)L.ytok[s0 >> 1] : d.blank;
+      const int l2 = (s0 & 1) ? (int)L.ytok[(s0 - 2) >> 1] : d.blank;
+      out.skip_ok = (int16_t)(l0 != d.blank && l0 != l2);
+    }
   }
   if (tid == 0) store_pod(glb(p.slots) + slot_index, out);
 }
-
-// Label of state s read straight from the int64 targets (tail fast path).
-__device__ inline int label_at(const GLB int64_t* y, int blank, int s) { return (s & 1) ? (int)y[s >> 1] : blank; }
 
 // Optimized mode, one workgroup per record, after the chunk kernel: repair
 // rounds, seam validation, full-DP fallback, final path and every per-record
@@ -1627,13 +1634,7 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) tail_kernel(Params p) {
         bool ok = !valid || isfinite(sk.objective);
         if (valid && k > 0) {  // legal_seam, cu:157-161
           const int jump = sk.start - end_prev;
-          bool seam = jump == 0 || jump == 1;
-          if (jump == 2) {
-            const GLB int64_t* y = glb(d.targets);
-            const int ls = label_at(y, d.blank, sk.start);
-            seam = ls != d.blank && ls != label_at(y, d.blank, sk.start - 2);
-          }
-          ok = ok && seam;
+          ok = ok && (jump == 0 || jump == 1 || (jump == 2 && sk.skip_ok));
         }
         if (__ballot(!ok) == 0) {
           float total = 0.0f;  // cu:578-584: chunk objectives summed in chunk order
@@ -1870,7 +1871,7 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
   std::memset(plan, 0, sizeof(*plan));
   plan->count = count;
   plan->total_frames = total_frames;
-  plan->table_bytes = count * (int64_t)sizeof(ffa::RecordDesc) + (int64_t)sizeof(ffa::ChunkDesc) * slots;
+  plan->table_bytes = count * (int64_t)sizeof(ffa::RecordDesc) + (int64_t)sizeof(ffa::ChunkEntry) * slots;
   plan->workspace_bytes = std::max<int64_t>(ws, 256);
   plan->reuse_rows = frontier ? count : 0;
   int64_t* in = plan->internal;
@@ -1903,7 +1904,7 @@ int ffa_align_describe(const ffa_align_plan* plan, const ffa_record* records, vo
   const bool frontier = in[I_FRONTIER] != 0;
   const int64_t H = in[I_H];
   auto* desc = static_cast<ffa::RecordDesc*>(host_table);
-  auto* chunks = reinterpret_cast<ffa::ChunkDesc*>(desc + count);
+  auto* chunks = reinterpret_cast<ffa::ChunkEntry*>(desc + count);
   int64_t frame = 0, bp = 0, fr = 0;
   int32_t slot = 0;
   for (int64_t i = 0; i < count; ++i) {
@@ -1930,22 +1931,12 @@ int ffa_align_describe(const ffa_align_plan* plan, const ffa_record* records, vo
       // one frame per lane of two waves
       const bool fast = in[I_MODE] == 2 && H <= 128 && r.vocab <= 32 && r.vocab % 4 == 0 &&
                         (reinterpret_cast<uintptr_t>(r.emissions) & 15) == 0;
+      const uint32_t tag = fast ? (ffa::CHUNK_FAST | (uint32_t)(r.vocab / 4 - 1) << 25) : 0u;
       for (int64_t c = 0; c < n; ++c) {
-        ffa::ChunkDesc& e = chunks[slot + c];
-        std::memset(&e, 0, sizeof(e));
+        ffa::ChunkEntry& e = chunks[slot + c];
         e.rows = r.emissions + c * H * r.vocab;
-        e.targets = r.targets;
-        e.out = frame + c * H;
-        e.frames = (int32_t)r.frames;
-        e.tokens = (int32_t)r.tokens;
-        e.vocab = (int32_t)r.vocab;
-        e.blank = (int32_t)r.blank;
-        e.record = (int32_t)i;
+        e.word = (uint32_t)i | (uint32_t)(std::min<int64_t>(H, r.frames - c * H) - 1) << 16 | tag;
         e.chunk = (int32_t)c;
-        e.n = (int32_t)std::min<int64_t>(H, r.frames - c * H);
-        e.flags = fast ? ffa::CHUNK_FAST : 0;
-        e.nchunks = (int32_t)n;
-        e.first_slot = slot;
       }
       slot += (int32_t)n;
     }
@@ -1969,7 +1960,7 @@ extern "C" int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_opti
   if (o->mode != in[I_MODE] || o->chunk_frames != in[I_H]) return fail(FFA_E_INVALID, "options differ from the plan");
   ffa::Params p{};
   p.desc = static_cast<const ffa::RecordDesc*>(device_table);
-  p.chunks = reinterpret_cast<const ffa::ChunkDesc*>(p.desc + plan->count);
+  p.chunks = reinterpret_cast<const ffa::ChunkEntry*>(p.desc + plan->count);
   p.validity = emission_validity;
   p.labels = out->labels;
   p.scores = out->scores;

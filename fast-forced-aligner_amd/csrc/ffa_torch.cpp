@@ -1,18 +1,27 @@
-// PyTorch operator registration for the MI355X alignment library.
+// PyTorch adaptor for the MI355X alignment library.
 //
 // Registers fast_forced_aligner_cuda::align and ::emission_validity with the
 // schemas of the reference (src/fast_forced_aligner/csrc/alignment.cu:1064-1070),
-// so a Python layer written against the reference's operators works unchanged.
-// This file only adapts tensors to the C ABI of include/ffa.h: it checks
-// arguments, builds the descriptor table in pinned host memory, uploads it
-// asynchronously, allocates outputs and scratch from PyTorch's caching
-// allocator, and enqueues the HIP kernels on the current stream. It never
-// synchronizes the host.
+// so a Python layer written against the reference's operators works unchanged,
+// and exposes the same alignment as a Python function (module _ffa_torch,
+// function align) that the package's own align() calls: it reads the Python
+// lists directly and skips the dispatcher's boxing of two tensor lists and
+// twenty arguments.
+//
+// Both entry points share one implementation that only adapts tensors to the
+// C ABI of include/ffa.h: it checks arguments, writes the descriptor table into
+// pinned host memory and uploads it asynchronously, allocates the scratch and
+// the outputs from PyTorch's caching allocator (one block each), and enqueues
+// the HIP kernels on the current stream. It never synchronizes the host.
 #include <ATen/ATen.h>
+#include <ATen/core/CachingHostAllocator.h>
 #include <ATen/hip/impl/HIPCachingAllocatorMasqueradingAsCUDA.h>
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+#include <c10/core/InferenceMode.h>
+#include <torch/csrc/autograd/python_variable.h>
 #include <torch/library.h>
+#include <pybind11/pybind11.h>
 
 #include <climits>
 #include <optional>
@@ -21,6 +30,8 @@
 
 #include "ffa.h"
 
+namespace py = pybind11;
+
 namespace {
 
 using c10::hip::HIPCachingAllocatorMasqueradingAsCUDA::recordStreamMasqueradingAsCUDA;
@@ -28,6 +39,126 @@ using c10::hip::HIPStreamMasqueradingAsCUDA;
 
 void check_ffa(int rc) {
   TORCH_CHECK(rc == FFA_OK, "fast_forced_aligner: ", ffa_last_error());
+}
+
+int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+
+// A tensor over bytes [offset, offset + numel*itemsize) of `block`: shares the
+// block's storage (one allocation serves every output of a call).
+at::Tensor view_of(const at::Tensor& block, int64_t offset, at::ScalarType type, c10::IntArrayRef sizes) {
+  const auto meta = c10::scalarTypeToTypeMeta(type);
+  auto t = at::detail::make_tensor<c10::TensorImpl>(c10::Storage(block.storage()), block.key_set(), meta);
+  t.unsafeGetTensorImpl()->set_storage_offset(offset / (int64_t)meta.itemsize());
+  t.unsafeGetTensorImpl()->set_sizes_contiguous(sizes);
+  return t;
+}
+
+// The alignment of one batch (alignment.cu:919-1061). `emission(i)` /
+// `target(i)` return the i-th input tensors, `blank(i)` its blank id.
+// Metadata errors raise ValueError with the reference Python layer's messages
+// (alignment.py:233-252); knob errors raise RuntimeError as the operator does.
+template <class E, class Y, class L>
+std::tuple<std::vector<at::Tensor>, std::vector<int64_t>> run_align(int64_t count, E emission, Y target, L blank,
+                                                                    const ffa_align_options& o,
+                                                                    const at::Tensor* validity) {
+  TORCH_CHECK_VALUE(count > 0 && count <= FFA_MAX_BATCH, "provide 1..65535 matching emissions and targets");
+  const at::Tensor& e0 = emission(0);
+  TORCH_CHECK_VALUE(e0.is_cuda(), "inputs must be contiguous CUDA float32 [T,V] and int64 [U] on one device");
+  const auto device = e0.device();
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(device);
+  const HIPStreamMasqueradingAsCUDA stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(device.index());
+  std::vector<ffa_record> records(count);
+  std::vector<int64_t> sizes(count);
+  const void* last_e = nullptr;
+  const void* last_y = nullptr;
+  for (int64_t i = 0; i < count; ++i) {
+    const at::Tensor& e = emission(i);
+    const at::Tensor& t = target(i);
+    const int64_t b = blank(i);
+    // the per-record metadata contract of alignment.py:243-251
+    TORCH_CHECK_VALUE(e.is_cuda() && e.device() == device && t.device() == device && e.scalar_type() == at::kFloat &&
+                          t.scalar_type() == at::kLong && e.dim() == 2 && t.dim() == 1 && e.is_contiguous() &&
+                          t.is_contiguous(),
+                      "inputs must be contiguous CUDA float32 [T,V] and int64 [U] on one device");
+    TORCH_CHECK_VALUE(e.size(0) > 0 && e.size(0) <= INT_MAX && e.size(1) > 0 && e.size(1) <= FFA_MAX_VOCAB &&
+                          2 * t.numel() + 1 <= FFA_MAX_STATES && b >= 0 && b < e.size(1),
+                      "unsupported frame count, vocabulary, target length, or blank ID");
+    records[i].emissions = static_cast<const float*>(e.data_ptr());
+    records[i].targets = t.numel() ? static_cast<const int64_t*>(t.data_ptr()) : nullptr;
+    records[i].frames = e.size(0);
+    records[i].vocab = e.size(1);
+    records[i].tokens = t.numel();
+    records[i].blank = b;
+    sizes[i] = e.size(0);
+    // the kernels read raw addresses: keep the sources alive for this stream
+    // (alignment.cu:977-980); consecutive views of one block are recorded once
+    const void* es = e.storage().data_ptr().get();
+    if (es != last_e) recordStreamMasqueradingAsCUDA(e.storage().data_ptr(), stream);
+    last_e = es;
+    if (t.numel()) {
+      const void* ys = t.storage().data_ptr().get();
+      if (ys != last_y) recordStreamMasqueradingAsCUDA(t.storage().data_ptr(), stream);
+      last_y = ys;
+    }
+  }
+  const uint8_t* mask = nullptr;  // checked after the records, as alignment.py:486-492 follows _metadata
+  if (validity) {
+    const at::Tensor& m = *validity;
+    TORCH_CHECK_VALUE(m.device() == device && m.scalar_type() == at::kBool && m.dim() == 1 && m.numel() == count &&
+                          m.is_contiguous(),
+                      "emission_validity must be contiguous CUDA bool [batch] on the input device");
+    recordStreamMasqueradingAsCUDA(m.storage().data_ptr(), stream);
+    mask = reinterpret_cast<const uint8_t*>(m.data_ptr());
+  }
+  ffa_align_plan plan;
+  check_ffa(ffa_align_plan_batch(records.data(), count, &o, &plan));
+  // descriptor table: pinned host block, uploaded on the stream into the head
+  // of the scratch allocation; the block is not reused before the copy ran
+  auto* host_alloc = at::getHostAllocator(at::kCUDA);
+  c10::DataPtr host = host_alloc->allocate(plan.table_bytes);
+  check_ffa(ffa_align_describe(&plan, records.data(), host.get(), plan.table_bytes));
+  const int64_t table_bytes = align256(plan.table_bytes);
+  const auto options = e0.options();
+  auto scratch = at::empty({table_bytes + plan.workspace_bytes}, options.dtype(at::kByte));
+  auto* scratch_ptr = static_cast<uint8_t*>(scratch.data_ptr());
+  const hipError_t copied = hipMemcpyAsync(scratch_ptr, host.get(), plan.table_bytes, hipMemcpyHostToDevice,
+                                           stream.stream());
+  TORCH_CHECK(copied == hipSuccess, "fast_forced_aligner: descriptor upload failed: ", hipGetErrorString(copied));
+  host_alloc->record_event(host.get(), host.get_context(), stream.unwrap());
+  // outputs: one allocation, ten views (alignment.cu:1059 order)
+  const int64_t N = plan.total_frames, B = count, R = plan.reuse_rows;
+  int64_t off = 0;
+  auto place = [&](int64_t bytes) { const int64_t at = off; off += align256(bytes); return at; };
+  const int64_t o_labels = place(8 * N), o_scores = place(4 * N), o_status = place(4 * B), o_objective = place(4 * B),
+                o_stitched = place(4 * B), o_passes = place(4 * B), o_repaired = place(8 * B),
+                o_shortcut = place(24 * B), o_routing = place(12 * B), o_reuse = place(32 * R);
+  auto block = at::empty({off}, options.dtype(at::kByte));
+  auto labels = view_of(block, o_labels, at::kLong, {N});
+  auto scores = view_of(block, o_scores, at::kFloat, {N});
+  auto status = view_of(block, o_status, at::kInt, {B});
+  auto objective = view_of(block, o_objective, at::kFloat, {B});
+  auto stitched = view_of(block, o_stitched, at::kInt, {B});
+  auto repair_passes = view_of(block, o_passes, at::kInt, {B});
+  auto repaired_frames = view_of(block, o_repaired, at::kLong, {B});
+  auto shortcut_stats = view_of(block, o_shortcut, at::kLong, {B, 3});
+  auto routing_stats = view_of(block, o_routing, at::kInt, {B, 3});
+  auto reuse_stats = view_of(block, o_reuse, at::kLong, {R, 4});
+  auto* base = static_cast<uint8_t*>(block.data_ptr());
+  ffa_align_outputs out;
+  out.labels = reinterpret_cast<int64_t*>(base + o_labels);
+  out.scores = reinterpret_cast<float*>(base + o_scores);
+  out.status = reinterpret_cast<int32_t*>(base + o_status);
+  out.objective = reinterpret_cast<float*>(base + o_objective);
+  out.stitched = reinterpret_cast<int32_t*>(base + o_stitched);
+  out.repair_passes = reinterpret_cast<int32_t*>(base + o_passes);
+  out.repaired_frames = reinterpret_cast<int64_t*>(base + o_repaired);
+  out.shortcut_stats = reinterpret_cast<int64_t*>(base + o_shortcut);
+  out.routing_stats = reinterpret_cast<int32_t*>(base + o_routing);
+  out.reuse_stats = R ? reinterpret_cast<int64_t*>(base + o_reuse) : nullptr;
+  check_ffa(ffa_align_launch(&plan, &o, scratch_ptr, mask, &out, scratch_ptr + table_bytes, stream.stream()));
+  return {{labels, scores, status, objective, stitched, repair_passes, repaired_frames, shortcut_stats,
+           routing_stats, reuse_stats},
+          std::move(sizes)};
 }
 
 // emission_validity (alignment.cu:893-917).
@@ -56,8 +187,8 @@ at::Tensor emission_validity(at::TensorList emissions) {
   return result;
 }
 
-// align (alignment.cu:919-1061).
-std::tuple<std::vector<at::Tensor>, std::vector<int64_t>> align(
+// align operator (alignment.cu:919-1061): the reference schema and return order.
+std::tuple<std::vector<at::Tensor>, std::vector<int64_t>> align_op(
     at::TensorList emissions, at::TensorList targets, at::IntArrayRef blanks, int64_t chunk_frames, int64_t mode,
     int64_t threads, int64_t repair_rounds, int64_t optimization_pass, int64_t variant,
     int64_t repair_budget_frames, int64_t repair_threads, bool compact_alphabet, bool parallel_traceback,
@@ -67,19 +198,6 @@ std::tuple<std::vector<at::Tensor>, std::vector<int64_t>> align(
   TORCH_CHECK_VALUE(count > 0 && count <= FFA_MAX_BATCH && (int64_t)targets.size() == count,
                     "provide 1..65535 matching emissions and targets");
   TORCH_CHECK_VALUE((int64_t)blanks.size() == count, "provide one blank ID per record");
-  TORCH_CHECK(emissions[0].is_cuda(), "CUDA emissions required");
-  const auto device = emissions[0].device();
-  c10::hip::HIPGuardMasqueradingAsCUDA guard(device);
-  const HIPStreamMasqueradingAsCUDA stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(device.index());
-  const uint8_t* mask = nullptr;
-  if (emission_validity.has_value()) {
-    const auto& m = *emission_validity;
-    TORCH_CHECK_VALUE(m.device() == device && m.scalar_type() == at::kBool && m.dim() == 1 && m.numel() == count &&
-                          m.is_contiguous(),
-                      "emission_validity must be contiguous CUDA bool [batch] on the input device");
-    recordStreamMasqueradingAsCUDA(m.storage().data_ptr(), stream);
-    mask = reinterpret_cast<const uint8_t*>(m.data_ptr<bool>());
-  }
   ffa_align_options o;
   ffa_default_options(mode != 0, &o);
   o.chunk_frames = chunk_frames;
@@ -98,63 +216,85 @@ std::tuple<std::vector<at::Tensor>, std::vector<int64_t>> align(
   o.frontier_reuse = frontier_reuse;
   o.frontier_min_frames = frontier_min_frames;
   o.check_inputs = check_inputs;
-  std::vector<ffa_record> records(count);
-  std::vector<int64_t> sizes(count);
-  for (int64_t i = 0; i < count; ++i) {
-    const auto& e = emissions[i];
-    const auto& t = targets[i];
-    // the per-record metadata contract of alignment.py:243-251, raised as ValueError
-    TORCH_CHECK_VALUE(e.is_cuda() && e.device() == device && t.device() == device && e.scalar_type() == at::kFloat &&
-                          t.scalar_type() == at::kLong && e.dim() == 2 && t.dim() == 1 && e.is_contiguous() &&
-                          t.is_contiguous(),
-                      "inputs must be contiguous CUDA float32 [T,V] and int64 [U] on one device");
-    TORCH_CHECK_VALUE(e.size(0) > 0 && e.size(0) <= INT_MAX && e.size(1) > 0 && e.size(1) <= FFA_MAX_VOCAB &&
-                          2 * t.numel() + 1 <= FFA_MAX_STATES && blanks[i] >= 0 && blanks[i] < e.size(1),
-                      "unsupported frame count, vocabulary, target length, or blank ID");
-    records[i].emissions = e.data_ptr<float>();
-    records[i].targets = t.numel() ? t.data_ptr<int64_t>() : nullptr;
-    records[i].frames = e.size(0);
-    records[i].vocab = e.size(1);
-    records[i].tokens = t.numel();
-    records[i].blank = blanks[i];
-    sizes[i] = e.size(0);
-    // the kernels read raw addresses: keep the sources alive for this stream (alignment.cu:977-980)
-    recordStreamMasqueradingAsCUDA(e.storage().data_ptr(), stream);
-    if (t.numel()) recordStreamMasqueradingAsCUDA(t.storage().data_ptr(), stream);
+  return run_align(
+      count, [&](int64_t i) -> const at::Tensor& { return emissions[i]; },
+      [&](int64_t i) -> const at::Tensor& { return targets[i]; }, [&](int64_t i) { return blanks[i]; }, o,
+      emission_validity.has_value() ? &*emission_validity : nullptr);
+}
+
+// Python entry of the package's align(): emissions / targets are Python
+// sequences of tensors, blank_id an int or a sequence of ints, and the knob
+// vector is the public API's (alignment.py:496-501). Returns the ten output
+// tensors and the record lengths. Outputs are inference tensors, as under the
+// reference's @torch.inference_mode.
+py::tuple align_py(py::handle emissions, py::handle targets, py::handle blank_id, bool optimized,
+                   bool check_inputs, py::handle validity) {
+  c10::InferenceMode inference;
+  py::object es_seq = py::reinterpret_steal<py::object>(PySequence_Fast(emissions.ptr(), "emissions"));
+  py::object ys_seq = py::reinterpret_steal<py::object>(PySequence_Fast(targets.ptr(), "targets"));
+  if (!es_seq || !ys_seq) throw py::error_already_set();
+  const int64_t count = PySequence_Fast_GET_SIZE(es_seq.ptr());
+  if (count <= 0 || count > FFA_MAX_BATCH || PySequence_Fast_GET_SIZE(ys_seq.ptr()) != count)
+    throw py::value_error("provide 1..65535 matching emissions and targets");
+  PyObject** es = PySequence_Fast_ITEMS(es_seq.ptr());
+  PyObject** ys = PySequence_Fast_ITEMS(ys_seq.ptr());
+  for (int64_t i = 0; i < count; ++i)
+    if (!THPVariable_Check(es[i]) || !THPVariable_Check(ys[i]))
+      throw py::value_error("inputs must be contiguous CUDA float32 [T,V] and int64 [U] on one device");
+  int64_t single = 0;
+  std::vector<int64_t> blanks;
+  auto as_blank = [](PyObject* x, int64_t* value) {  // an int, not a bool (alignment.py:250)
+    if (!PyLong_Check(x) || PyBool_Check(x)) return false;
+    int overflow = 0;
+    *value = PyLong_AsLongLongAndOverflow(x, &overflow);
+    return overflow == 0 && !(*value == -1 && PyErr_Occurred());
+  };
+  const bool uniform = PyLong_Check(blank_id.ptr()) && !PyBool_Check(blank_id.ptr());
+  if (uniform) {
+    if (!as_blank(blank_id.ptr(), &single)) {
+      PyErr_Clear();
+      throw py::value_error("unsupported frame count, vocabulary, target length, or blank ID");
+    }
+  } else {
+    py::object bs = py::reinterpret_steal<py::object>(PySequence_Fast(blank_id.ptr(), "blank_id"));
+    if (!bs) throw py::error_already_set();
+    if (PySequence_Fast_GET_SIZE(bs.ptr()) != count) throw py::value_error("provide one blank ID per record");
+    blanks.resize(count);
+    PyObject** items = PySequence_Fast_ITEMS(bs.ptr());
+    for (int64_t i = 0; i < count; ++i)
+      if (!as_blank(items[i], &blanks[i])) {
+        PyErr_Clear();
+        throw py::value_error("unsupported frame count, vocabulary, target length, or blank ID");
+      }
   }
-  ffa_align_plan plan;
-  check_ffa(ffa_align_plan_batch(records.data(), count, &o, &plan));
-  auto host = at::empty({plan.table_bytes}, at::TensorOptions().dtype(at::kByte).device(at::kCPU).pinned_memory(true));
-  check_ffa(ffa_align_describe(&plan, records.data(), host.data_ptr(), plan.table_bytes));
-  auto table = host.to(device, /*non_blocking=*/true);
-  const auto options = emissions[0].options();
-  auto empty = [&](at::IntArrayRef shape, at::ScalarType type) { return at::empty(shape, options.dtype(type)); };
-  auto labels = empty({plan.total_frames}, at::kLong);
-  auto scores = empty({plan.total_frames}, at::kFloat);
-  auto status = empty({count}, at::kInt);
-  auto objective = empty({count}, at::kFloat);
-  auto stitched = empty({count}, at::kInt);
-  auto repair_passes = empty({count}, at::kInt);
-  auto repaired_frames = empty({count}, at::kLong);
-  auto shortcut_stats = empty({count, 3}, at::kLong);
-  auto routing_stats = empty({count, 3}, at::kInt);
-  auto reuse_stats = empty({plan.reuse_rows, 4}, at::kLong);
-  auto workspace = empty({plan.workspace_bytes}, at::kByte);
-  ffa_align_outputs out;
-  out.labels = labels.data_ptr<int64_t>();
-  out.scores = scores.data_ptr<float>();
-  out.status = status.data_ptr<int32_t>();
-  out.objective = objective.data_ptr<float>();
-  out.stitched = stitched.data_ptr<int32_t>();
-  out.repair_passes = repair_passes.data_ptr<int32_t>();
-  out.repaired_frames = repaired_frames.data_ptr<int64_t>();
-  out.shortcut_stats = shortcut_stats.data_ptr<int64_t>();
-  out.routing_stats = routing_stats.data_ptr<int32_t>();
-  out.reuse_stats = plan.reuse_rows ? reuse_stats.data_ptr<int64_t>() : nullptr;
-  check_ffa(ffa_align_launch(&plan, &o, table.data_ptr(), mask, &out, workspace.data_ptr(), stream.stream()));
-  return {{labels, scores, status, objective, stitched, repair_passes, repaired_frames, shortcut_stats,
-           routing_stats, reuse_stats},
-          std::move(sizes)};
+  const at::Tensor* mask = nullptr;
+  if (!validity.is_none()) {
+    if (!THPVariable_Check(validity.ptr()))
+      throw py::value_error("emission_validity must be contiguous CUDA bool [batch] on the input device");
+    mask = &THPVariable_Unpack(validity.ptr());
+  }
+  ffa_align_options o;
+  ffa_default_options(optimized ? 1 : 0, &o);
+  o.check_inputs = check_inputs;
+  std::tuple<std::vector<at::Tensor>, std::vector<int64_t>> result;
+  try {
+    result = run_align(
+        count, [&](int64_t i) -> const at::Tensor& { return THPVariable_Unpack(es[i]); },
+        [&](int64_t i) -> const at::Tensor& { return THPVariable_Unpack(ys[i]); },
+        [&](int64_t i) { return uniform ? single : blanks[i]; }, o, mask);
+  } catch (const c10::ValueError& error) {
+    throw py::value_error(error.what_without_backtrace());
+  } catch (const c10::Error& error) {
+    throw std::runtime_error(error.what_without_backtrace());
+  }
+  const auto& tensors = std::get<0>(result);
+  const auto& lengths = std::get<1>(result);
+  py::tuple outs(tensors.size());
+  for (size_t i = 0; i < tensors.size(); ++i)
+    outs[i] = py::reinterpret_steal<py::object>(THPVariable_Wrap(tensors[i]));
+  py::tuple lens(lengths.size());
+  for (size_t i = 0; i < lengths.size(); ++i) lens[i] = py::int_(lengths[i]);
+  return py::make_tuple(outs, lens);
 }
 
 }  // namespace
@@ -169,6 +309,12 @@ TORCH_LIBRARY(fast_forced_aligner_cuda, m) {
 }
 
 TORCH_LIBRARY_IMPL(fast_forced_aligner_cuda, CUDA, m) {
-  m.impl("align", &align);
+  m.impl("align", &align_op);
   m.impl("emission_validity", &emission_validity);
+}
+
+PYBIND11_MODULE(_ffa_torch, m) {
+  m.doc() = "MI355X CTC forced alignment: the package's direct entry to the HIP library";
+  m.def("align", &align_py, py::arg("emissions"), py::arg("targets"), py::arg("blank_id"), py::arg("optimized"),
+        py::arg("check_inputs"), py::arg("emission_validity"));
 }

@@ -32,6 +32,9 @@ def _rocm_home() -> Path | None:
     return Path(home) if home else None
 
 
+_native = None  # the _ffa_torch module once load_extension() succeeded
+
+
 @lru_cache(maxsize=1)
 def load_extension() -> None:
     """Load the bundled HIP extension (build it first if it is absent).
@@ -64,9 +67,13 @@ def load_extension() -> None:
         module = importlib.util.module_from_spec(spec)
         spec.loader.exec_module(module)
         module.build()
-    # the HIP library first, so the operator library resolves against it
+    # the HIP library first, so the operator library resolves against it;
+    # importing _ffa_torch registers the fast_forced_aligner_cuda operators
     ctypes.CDLL(str(HIP_LIBRARY), mode=ctypes.RTLD_GLOBAL)
-    torch.ops.load_library(str(TORCH_LIBRARY))
+    global _native
+    from . import _ffa_torch
+
+    _native = _ffa_torch
 
 
 @dataclass(frozen=True)
@@ -154,22 +161,6 @@ def _metadata(emissions: Sequence[Tensor], targets: Sequence[Tensor],
 MAX_TOKENS = 10239
 
 
-def _blank_list(emissions: Sequence[Tensor], targets: Sequence[Tensor],
-                blank_id: int | Sequence[int]) -> list[int]:
-    """The O(1)-per-record part of ``_metadata``: batch size and blank types."""
-    count = len(emissions)
-    if not 0 < count <= 65535 or len(targets) != count:
-        raise ValueError("provide 1..65535 matching emissions and targets")
-    if type(blank_id) is int:
-        return [blank_id] * count
-    blanks = list(blank_id)
-    if len(blanks) != count:
-        raise ValueError("provide one blank ID per record")
-    if not all(type(b) is int for b in blanks):
-        raise ValueError("unsupported frame count, vocabulary, target length, or blank ID")
-    return blanks
-
-
 @torch.inference_mode()
 def validate_inputs(emissions: Sequence[Tensor], targets: Sequence[Tensor], *,
                     blank_id: int | Sequence[int] = 0) -> None:
@@ -209,7 +200,6 @@ def emission_validity(emissions: Sequence[Tensor]) -> Tensor:
         return torch.ops.fast_forced_aligner_cuda.emission_validity(list(emissions))
 
 
-@torch.inference_mode()
 def align(emissions: Sequence[Tensor], targets: Sequence[Tensor], *,
           blank_id: int | Sequence[int] = 0, mode: Mode = "optimized",
           check_inputs: bool = True, emission_validity: Tensor | None = None) -> AlignmentBatch:
@@ -227,6 +217,8 @@ def align(emissions: Sequence[Tensor], targets: Sequence[Tensor], *,
 
     Returns:
         AlignmentBatch; failures are reported in ``status``, never raised here.
+        Its tensors are inference tensors, as under the reference's
+        ``torch.inference_mode``.
 
     Raises:
         ValueError: invalid mode, metadata, blank ids or mask metadata.
@@ -237,26 +229,11 @@ def align(emissions: Sequence[Tensor], targets: Sequence[Tensor], *,
         raise ValueError("mode must be 'optimized' or 'conventional'")
     if type(check_inputs) is not bool:
         raise TypeError("check_inputs must be bool")
-    if emissions and isinstance(emissions[0], Tensor) and emissions[0].is_cuda:
-        # The native operator checks every record's metadata with the same
-        # messages and raises ValueError (O(B) in C++ instead of Python).
-        blanks = _blank_list(emissions, targets, blank_id)
-    else:
-        blanks = _metadata(emissions, targets, blank_id)
-    if emission_validity is not None:
-        if (not isinstance(emission_validity, Tensor)
-                or emission_validity.device != emissions[0].device
-                or emission_validity.dtype != torch.bool or emission_validity.ndim != 1
-                or emission_validity.numel() != len(emissions)
-                or not emission_validity.is_contiguous()):
-            raise ValueError("emission_validity must be contiguous CUDA bool [batch] on the input device")
+    if not (emissions and isinstance(emissions[0], Tensor) and emissions[0].is_cuda):
+        _metadata(emissions, targets, blank_id)  # raises the reference's ValueError for these inputs
     load_extension()
-    optimized = mode == "optimized"
-    # the fixed knob vector of py:496-501; the operator guards the input device
-    tensors, lengths = torch.ops.fast_forced_aligner_cuda.align(
-        list(emissions), list(targets), blanks,
-        128, 2 if optimized else 0, 512, 2, 2, 2,
-        512 if optimized else 0, 0, False, True, optimized,
-        2048, 2048, optimized, 2048, emission_validity, check_inputs,
-    )
-    return AlignmentBatch(tuple(lengths), *tensors)
+    # the native entry checks every record's metadata with the same messages
+    # (O(B) in C++) and passes the fixed knob vector of py:496-501
+    tensors, lengths = _native.align(emissions, targets, blank_id, mode == "optimized", check_inputs,
+                                     emission_validity)
+    return AlignmentBatch(lengths, *tensors)

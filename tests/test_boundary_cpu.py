@@ -77,8 +77,8 @@ def test_plan_sizes_and_gating(lib):
     assert rc == 0
     assert plan.count == 2 and plan.total_frames == 820
     slots = 4 + 3  # ceil(T/128)
-    # 64-byte record descriptors and 64-byte chunk descriptors
-    assert plan.table_bytes == 2 * 64 + 64 * slots
+    # 64-byte record descriptors and 16-byte chunk entries
+    assert plan.table_bytes == 2 * 64 + 16 * slots
     assert plan.reuse_rows == 0
     rc, plan, _ = _plan(lib, [(2048, 32, 4, 0), (320, 32, 3, 0)])
     assert rc == 0 and plan.reuse_rows == 2  # frontier reuse: batch max T >= 2048 (alignment.cu:1002)

@@ -153,6 +153,29 @@ def test_blank_inside_targets_unchecked():
     assert got["shortcut_stats"][0, 2] >= 1  # the all-blank opening chunk is ambiguous
 
 
+@pytest.mark.parametrize("mode", ["conventional", "optimized"])
+def test_reference_operator_matches_package_entry(mode):
+    """The operator with the reference schema (alignment.cu:1064-1070), called
+    the way the reference's Python layer calls it (alignment.py:496-501),
+    returns the same ten tensors and lengths as the package's direct entry."""
+    b = workloads.c2(batch=12)
+    es = [torch.from_numpy(e).to(DEV) for e in b.emissions]
+    ys = [torch.from_numpy(y).to(DEV) for y in b.targets]
+    ys[3] = torch.tensor([1, 40], device=DEV)  # a rejected record (status 3)
+    optimized = mode == "optimized"
+    got = ffa.align(es, ys, mode=mode)
+    with torch.inference_mode():
+        tensors, lengths = torch.ops.fast_forced_aligner_cuda.align(
+            es, ys, [0] * len(es), 128, 2 if optimized else 0, 512, 2, 2, 2, 512 if optimized else 0, 0, False,
+            True, optimized, 2048, 2048, optimized, 2048, None, True)
+    assert tuple(lengths) == got.lengths
+    for name, tensor in zip(FIELDS, tensors):
+        mine = getattr(got, name)
+        assert mine.dtype == tensor.dtype and mine.shape == tensor.shape, name
+        assert torch.equal(mine, tensor), name
+    assert got.status.tolist()[3] == 3
+
+
 def test_c_abi_direct_call():
     """Drive the HIP library through its C entry points (ctypes), with caller-
     allocated device buffers, and compare with the oracle."""
