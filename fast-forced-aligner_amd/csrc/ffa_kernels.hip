@@ -44,6 +44,7 @@ constexpr float NEG_INF = -INFINITY;
 constexpr int MAX_H = 512;          // chunk_frames supported by the LDS layout
 constexpr int TAIL_SLOT_CAP = 512;  // record tails with more chunks plan in global memory
 constexpr int YTOK_PAD = 72;        // sentinel entries after the staged targets
+constexpr int EBLK_COLS = 64;       // widest row (V) staged in LDS blocks by the DP
 
 struct RecordDesc {  // device descriptor table entry, 64 bytes
   const float* emissions;
@@ -101,6 +102,7 @@ struct Params {
   int64_t budget, repair_min, frontier_min;
   int32_t count, total_slots, H, mode, repair_rounds, check_inputs, overlap, frontier_batch;
   int32_t u_cap, d_cap, v_words, lds_tail_slots;
+  int32_t eblk_frames;  // frames per LDS emission block of the DP (0: rows read straight from HBM)
 };
 
 // ---------------------------------------------------------------------------
@@ -126,6 +128,8 @@ struct Lds {
   Header* h;
   int16_t* ytok;   // targets as int16 (V <= 8192)
   uint16_t* key3;  // per target position j: key of y[j], y[j+1], y[j+2] (placement prefilter)
+  float* eblk;     // DP emission blocks: 2 halves of eblk_frames rows of up to EBLK_COLS values
+  int eblk_frames;
   // greedy region (aliased by the tail's slot copy)
   int32_t* g;
   float* fs;
@@ -155,6 +159,9 @@ __device__ inline Lds carve(unsigned char* base, const Params& p) {
   off = align16(off + 2 * ((size_t)p.u_cap + YTOK_PAD));
   L.key3 = reinterpret_cast<uint16_t*>(base + off);
   off = align16(off + 2 * ((size_t)p.u_cap + YTOK_PAD));
+  L.eblk = p.eblk_frames ? reinterpret_cast<float*>(base + off) : nullptr;
+  L.eblk_frames = p.eblk_frames;
+  off += (size_t)8 * p.eblk_frames * EBLK_COLS;
   unsigned char* region = base + off;
   size_t g = 0;
   const size_t h32 = (size_t)greedy_frames(p.H);
@@ -546,10 +553,61 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
       __syncthreads();
     }
   };
+  const int64_t last = b - 1;
+  if (L.eblk && V <= EBLK_COLS) {
+    // Emission rows staged in LDS, one block of F frames at a time (the block's
+    // rows are one contiguous span of F*V floats in HBM, so every thread loads
+    // plain coalesced dwords). Block k+1 is loaded into registers when block k
+    // starts and written to the other half of the double buffer after block
+    // k's frames are computed: each load has a whole block of frames to land,
+    // and no load result is carried across a loop iteration.
+    const int F = L.eblk_frames;
+    constexpr int EB = K == 4 ? 32 : 11;  // per-thread values of one block (blockDim >= 64 for K = 4, >= 192 otherwise)
+    const int NT = blockDim.x;
+    float buf[EB];
+    auto load_block = [&](int64_t tb) {
+      const int total = (int)(min(tb + F, b) - tb) * (int)V;
+      const GLB float* src = e + tb * V;
+#pragma unroll
+      for (int i = 0; i < EB; ++i) {
+        const int idx = tid + i * NT;
+        if (idx < total) buf[i] = src[idx];
+      }
+    };
+    auto store_block = [&](int64_t tb, float* half) {
+      const int total = (int)(min(tb + F, b) - tb) * (int)V;
+#pragma unroll
+      for (int i = 0; i < EB; ++i) {
+        const int idx = tid + i * NT;
+        if (idx < total) half[idx] = buf[i];
+      }
+    };
+    int half = 0;
+    if (start_t <= last) {
+      load_block(start_t);
+      store_block(start_t, L.eblk);
+      __syncthreads();
+    }
+    for (int64_t tb = start_t; tb <= last; tb += F) {
+      const int64_t nb = tb + F;
+      if (nb <= last) load_block(nb);
+      const float* rows = L.eblk + half * F * EBLK_COLS;
+      const int nf = (int)min((int64_t)F, last - tb + 1);
+      for (int f = 0; f < nf; ++f) {
+        float evk[K];
+        const float* row = rows + f * (int)V;
+#pragma unroll
+        for (int k = 0; k < K; ++k) evk[k] = *(const float*)((const char*)row + lab[k]);
+        frame(tb + f, evk);
+      }
+      if (nb <= last) store_block(nb, L.eblk + (half ^ 1) * F * EBLK_COLS);
+      __syncthreads();  // the next block is in LDS; this block's reads are done
+      half ^= 1;
+    }
+  } else {
   // Prefetch ring: the gathers of frame t are issued D frames ahead; loads past
   // the interval are clamped to its last row so every load is unconditional.
   // The main loop runs whole groups of D frames with no exits inside a group.
-  const int64_t last = b - 1;
   float ev[D][K];
 #pragma unroll
   for (int d = 0; d < D; ++d) {
@@ -571,6 +629,7 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
 #pragma unroll
   for (int d = 0; d < D; ++d)
     if (t0 + d < b) frame(t0 + d, ev[d]);
+  }
   if (save_frontier) {  // cu:451-454
 #pragma unroll
     for (int k = 0; k < K; ++k)
@@ -1729,7 +1788,7 @@ inline int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 // internal[] of ffa_align_plan
 enum {
   I_K, I_NT, I_SLOTS, I_LDS, I_UCAP, I_DCAP, I_VWORDS, I_TAILSLOTS, I_FRONTIER, I_BUDGET,
-  I_OVERLAP, I_WS_SLOTS, I_WS_FRONTIER, I_MODE, I_H, I_FMIN, I_REPAIR_MIN
+  I_OVERLAP, I_WS_SLOTS, I_WS_FRONTIER, I_MODE, I_H, I_FMIN, I_REPAIR_MIN, I_EBLK
 };
 
 template <int K, int D>
@@ -1826,6 +1885,7 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
   int64_t total_frames = 0, bp_words = 0, slots = 0, frontier_floats = 0;
   int64_t max_frames = 0, u_max = 0, v_max = 0, d_cap = 1, n_max = 0;
   int s_max = 1;
+  int64_t v_min = INT64_MAX;
   for (int64_t i = 0; i < count; ++i) {
     const ffa_record& r = records[i];
     if (r.frames <= 0 || r.frames > INT_MAX || r.vocab <= 0 || r.vocab > FFA_MAX_VOCAB || r.tokens < 0 ||
@@ -1841,6 +1901,7 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
     v_max = std::max(v_max, r.vocab);
     d_cap = std::max(d_cap, std::min(r.vocab, r.tokens + 1));
     s_max = std::max(s_max, S);
+    v_min = std::min(v_min, r.vocab);
     if (optimized) {
       const int64_t n = 1 + (r.frames - 1) / H;
       slots += n;
@@ -1861,8 +1922,15 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
   const int64_t greedy_bytes = 20 * ffa::greedy_frames(H) + 2048 + align_up(2 * d_cap, 16) + 8 * v_words;
   const int64_t region = std::max(greedy_bytes, 32 * tail_slots);
   const int64_t targets = align_up(2 * (std::max<int64_t>(u_max, 1) + ffa::YTOK_PAD), 16);
-  const int64_t lds = align_up((int64_t)sizeof(ffa::Header), 16) + 2 * targets + region;
+  int64_t lds = align_up((int64_t)sizeof(ffa::Header), 16) + 2 * targets + region;
   if (lds > 64 * 1024) return fail(FFA_E_INVALID, "batch needs more than 64 KiB of LDS per workgroup");
+  // DP emission blocks (two halves of F rows of up to 64 values) for records
+  // with V <= 64: 32 frames per block when the space fits, else 16, else none
+  int64_t eblk_frames = 0;
+  if (v_min <= ffa::EBLK_COLS)
+    for (int64_t f = 32; f >= 16 && !eblk_frames; f /= 2)
+      if (lds + 8 * f * ffa::EBLK_COLS <= 64 * 1024) eblk_frames = f;
+  lds += 8 * eblk_frames * ffa::EBLK_COLS;
   int64_t ws = align_up(4 * bp_words, 256);
   const int64_t ws_slots = ws;
   ws += align_up(32 * slots, 256);
@@ -1883,6 +1951,7 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
   in[I_DCAP] = d_cap;
   in[I_VWORDS] = v_words;
   in[I_TAILSLOTS] = tail_slots;
+  in[I_EBLK] = eblk_frames;
   in[I_FRONTIER] = frontier ? 1 : 0;
   in[I_BUDGET] = budget_on ? o->repair_budget_frames : 0;
   in[I_OVERLAP] = (budget_on && o->overlap_fallback) ? 1 : 0;
@@ -1991,6 +2060,7 @@ extern "C" int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_opti
   p.d_cap = (int32_t)in[I_DCAP];
   p.v_words = (int32_t)in[I_VWORDS];
   p.lds_tail_slots = (int32_t)in[I_TAILSLOTS];
+  p.eblk_frames = (int32_t)in[I_EBLK];
   const int NT = (int)in[I_NT];
   const size_t lds = (size_t)in[I_LDS];
   switch (in[I_K]) {

@@ -104,6 +104,20 @@ def test_config_parity(config, mode):
         assert all(s == 0 for s, k in zip(status, kinds) if k != "infeasible")
 
 
+@pytest.mark.parametrize("mode", ["conventional", "optimized"])
+def test_c3_long_form_parity(mode):
+    """Config C3 (4 x 30,000 frames, 9,000 tokens: 18,001 states, beyond the
+    reference's 4,096-state limit): all ten outputs bit-exact with the oracle,
+    including the T >= 2048 features (repair budget, early fallback, frontier
+    reuse) and the windowed traceback over 30,000 frames."""
+    b = workloads.make("c3")
+    print(f"c3 {mode}", flush=True)
+    got = compare(b.emissions, b.targets, mode=mode, where="c3")
+    assert (got["status"] == 0).all()
+    for p, y in zip(split(got["labels"], got["lengths"]), b.targets):
+        assert collapse(p, 0).tolist() == y.tolist()
+
+
 @pytest.mark.parametrize("config", ["c2", "c5"])
 def test_optimized_equals_conventional(config):
     b = workloads.make(config)
