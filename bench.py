@@ -31,9 +31,12 @@ METRIC = "aligned frames/sec + DP cells/sec on 1 MI355X; % of HBM roofline"
 HBM_PEAK_GBS = 8000.0
 
 
+HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000  # hip_runtime_api.h: timing-only events, no cache writeback
+
+
 def hip_runtime():
     lib = ctypes.CDLL("libamdhip64.so.7")
-    lib.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    lib.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
     lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
     lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
     return lib
@@ -48,7 +51,8 @@ def measure(ffa, capi_lib, hip, es, ys, mode, steps, warmup):
     starts, stops = [], []
     for _ in range(steps):
         a, b = ctypes.c_void_p(), ctypes.c_void_p()
-        assert hip.hipEventCreate(ctypes.byref(a)) == 0 and hip.hipEventCreate(ctypes.byref(b)) == 0
+        assert hip.hipEventCreateWithFlags(ctypes.byref(a), HIP_EVENT_DISABLE_SYSTEM_FENCE) == 0
+        assert hip.hipEventCreateWithFlags(ctypes.byref(b), HIP_EVENT_DISABLE_SYSTEM_FENCE) == 0
         starts.append(a)
         stops.append(b)
     torch.cuda.synchronize()
@@ -66,6 +70,20 @@ def measure(ffa, capi_lib, hip, es, ys, mode, steps, warmup):
         hip.hipEventDestroy(a)
         hip.hipEventDestroy(b)
     return elapsed / steps, sum(kernel_ms) / len(kernel_ms), result
+
+
+def measured_traffic(config, mode, kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summaries (a line
+    `traffic_bytes_per_launch[<config> <mode> <kernel>] = <bytes>`), or None."""
+    import re
+
+    key = f"{config} {mode} {kernel}"
+    for path in sorted((REPO / "profiles").glob("*traffic*.md")):
+        for m in re.finditer(r"traffic_bytes_per_launch\[(.+?)\] = (\d+)", path.read_text()):
+            if m.group(1) == key:
+                return int(m.group(2))
+    return None
 
 
 def cpu_baseline(batch, seconds=10.0):
@@ -130,6 +148,7 @@ def main() -> int:
         achieved = min_bytes / (kernel_ms * 1e-3) / 1e9
         return step_s, kernel_ms, achieved, result
 
+    kernel_name = "chunk_kernel" if args.mode == "optimized" else "conventional_kernel"
     step_s, kernel_ms, achieved, result = figures(args.mode, args.steps, args.warmup)
     # parity spot check outside the timed region
     from oracle import oracle
@@ -156,9 +175,9 @@ def main() -> int:
         "dp_cells_per_s": batch.cells / step_s,
         "parity_vs_oracle": parity,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": "chunk_kernel" if args.mode == "optimized" else "conventional_kernel",
-                     "kernel_us": kernel_ms * 1e3, "algorithmic_bytes": min_bytes},
+                     "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": measured_traffic(args.config, args.mode, kernel_name),
+                     "kernel": kernel_name, "kernel_us": kernel_ms * 1e3, "algorithmic_bytes": min_bytes},
     }
     if not args.no_conventional and args.mode == "optimized":
         c_step, c_kernel_ms, c_achieved, _ = figures("conventional", max(10, args.steps // 10), 3)
