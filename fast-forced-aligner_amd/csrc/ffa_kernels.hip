@@ -1085,6 +1085,9 @@ __device__ __attribute__((always_inline)) int place_wave(const Lds& L, int g0, i
                                                         bool at_start, bool at_end, bool small_vocab, int* start_out,
                                                         int* rlast_out) {
   const int lane = threadIdx.x & 63;
+  // keys of target positions 8*lane .. 8*lane+7, read before the pattern is
+  // known (most chunks need only this first block of 512 positions)
+  const v4i_t kv0 = *reinterpret_cast<const v4i_t*>(L.key3 + min(8 * lane, (U >> 3) << 3));
   const int gp0 = wave_shr1_int(g0, -1);
   const int gp1 = wave_shr1_int(g1, __builtin_amdgcn_readlane(g0, 63));
   auto step = [&](int f, int g, int gp, int& inc, int& tc) {
@@ -1107,9 +1110,9 @@ __device__ __attribute__((always_inline)) int place_wave(const Lds& L, int g0, i
     if (at_start || at_end) return 1;
     return min((S + 1) / 2, 2);
   }
-  // the pattern in LDS for the verification rounds
-  if (tc0) L.pc[(v0 >> 16) - 1] = g0;
-  if (tc1) L.pc[(v1 >> 16) - 1] = g1;
+  // pattern index of this lane's token change points (-1: none)
+  const int i0 = tc0 ? (v0 >> 16) - 1 : -1;
+  const int i1 = tc1 ? (v1 >> 16) - 1 : -1;
   // first three pattern tokens and r1 straight from the change-point masks
   uint64_t m0 = __ballot(tc0), m1 = __ballot(tc1);
   int c[3] = {0, 0, 0};
@@ -1133,10 +1136,12 @@ __device__ __attribute__((always_inline)) int place_wave(const Lds& L, int g0, i
   const int jhi = min(min(E, U - m), at_start ? 0 : INT_MAX);
   int matches = 0, start = -1;
   if (jlo > jhi) { *start_out = -1; return 0; }
-  const int pc_lo = lane < m ? L.pc[lane] : -3;
-  const int pc_hi = lane + 64 < m ? L.pc[lane + 64] : -3;
-  auto verify = [&](int j) {  // y[j .. j+m) == pattern, all lanes
-    const bool bad = (lane < m && L.ytok[j + lane] != pc_lo) || (lane + 64 < m && L.ytok[j + lane + 64] != pc_hi);
+  // y[j .. j+m) == pattern, checked in frame space: each change point compares
+  // its own label with the target at its pattern index (all lanes take part)
+  auto verify = [&](int j) {  // branch-free: both reads are in bounds (j + max(i, 0) < U)
+    const int y0 = L.ytok[j + max(i0, 0)];
+    const int y1 = L.ytok[j + max(i1, 0)];
+    const bool bad = ((i0 >= 0) & (y0 != g0)) | ((i1 >= 0) & (y1 != g1));
     return __ballot(bad) == 0;
   };
   if (m >= 3 && jhi - jlo >= 8) {
@@ -1145,13 +1150,13 @@ __device__ __attribute__((always_inline)) int place_wave(const Lds& L, int g0, i
     int total = 0;
     for (int base = jlo & ~7; base <= jhi; base += 512) {
       const int j0 = base + 8 * lane;
-      const v4i_t kv = *reinterpret_cast<const v4i_t*>(L.key3 + min(j0, (jhi & ~7)));
+      const v4i_t kv = base == 0 ? kv0 : *reinterpret_cast<const v4i_t*>(L.key3 + min(j0, (jhi & ~7)));
       uint32_t hits = 0;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const uint32_t key = ((uint32_t)kv[e >> 1] >> (16 * (e & 1))) & 0xffffu;
         const int j = j0 + e;
-        hits |= (uint32_t)(key == pkey && j >= jlo && j <= jhi) << e;
+        hits |= (uint32_t)((key == pkey) & (j >= jlo) & (j <= jhi)) << e;
       }
       const int cnt = __builtin_amdgcn_readlane(wave_scan_dpp(__popc(hits)), 63);
       if (cnt && total + cnt <= VERIFY_CAP) {
@@ -1191,8 +1196,10 @@ __device__ __attribute__((always_inline)) int place_wave(const Lds& L, int g0, i
     *start_out = start;
     return matches;
   }
-  // many candidates (repetitive transcripts) or m < 3: every position checked
-  // in full by its own lane
+  // many candidates (repetitive transcripts) or m < 3: the pattern in LDS and
+  // every position checked in full by its own lane
+  if (tc0) L.pc[i0] = g0;
+  if (tc1) L.pc[i1] = g1;
   for (int base = jlo; base <= jhi && matches < 2; base += 64) {  // uniform trip count for the ballots
     const int j = base + lane;
     bool hit = j <= jhi;
@@ -1268,7 +1275,7 @@ __device__ __attribute__((always_inline)) int greedy_fast(const Lds& L, const fl
     score = h->fbuf[1];
   } else {
     if (wave == 0) {
-      const int m = place_wave(L, L.g[lane], L.g[lane + 64], n, U, S, blank, at_start, at_end, V <= 32, &start, &rlast);
+      const int m = place_wave(L, g, L.g[lane + 64], n, U, S, blank, at_start, at_end, V <= 32, &start, &rlast);
       if (lane == 0) { h->ibuf[3] = m; h->ibuf[4] = start; h->ibuf[6] = rlast; }
     } else if (wave == 1 && lane == 0) {
       h->fbuf[1] = serial_sum128(L.fs);  // padding frames add -0.0, an exact identity
