@@ -86,6 +86,32 @@ def measured_traffic(config, mode, kernel):
     return None
 
 
+def extras(ffa, es, ys, result, steps=100):
+    """Pipelined per-call wall time of the path's neighbours on the same batch:
+    emission_validity (the NaN/+inf scan in front of align) and token_spans
+    (the timestamp epilogue after it)."""
+    import torch
+
+    def timed(fn):
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps
+
+    scan_bytes = sum(e.numel() * 4 for e in es)
+    t_scan = timed(lambda: ffa.emission_validity(es))
+    span_bytes = result.labels.numel() * 8 + sum(int(y.numel()) for y in ys) * 16
+    t_spans = timed(lambda: ffa.token_spans(result, ys))
+    return {"emission_validity": {"us_per_call": t_scan * 1e6, "bytes": scan_bytes,
+                                  "GB_per_s": scan_bytes / t_scan / 1e9},
+            "token_spans": {"us_per_call": t_spans * 1e6, "bytes": span_bytes,
+                            "GB_per_s": span_bytes / t_spans / 1e9}}
+
+
 def cpu_baseline(batch, seconds=10.0):
     """The oracle's conventional DP (same recurrence and tie rule as the
     reference's conventional mode) on host threads, one record per task."""
@@ -184,6 +210,7 @@ def main() -> int:
         line["conventional"] = {"ms_per_step": c_step * 1e3, "frames_per_s": batch.frames / c_step,
                                 "dp_cells_per_s": batch.cells / c_step, "kernel_us": c_kernel_ms * 1e3,
                                 "roofline_frac": c_achieved / HBM_PEAK_GBS}
+    line["extras"] = extras(ffa, es, ys, result)
     line["cpu_baseline"] = None if args.no_cpu else cpu_baseline(batch)
     if args.calibrate_copy > 0:
         src = torch.ones(args.calibrate_copy << 18, dtype=torch.float32, device=dev)

@@ -1748,6 +1748,66 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) tail_kernel(Params p) {
   }
 }
 
+// Token spans of one record per workgroup (the reference README's
+// "Converting frame labels to timestamps": split the path into equal-label
+// runs, drop blank runs, keep each run's start and exclusive end frame;
+// blank-separated repeats stay separate occurrences). A successful path has
+// exactly `tokens` such runs; the k-th run is written to spans[span_offset + k]
+// as {start, end}; rows past the last run (a transcript holding the blank id,
+// reachable only unchecked) and every row of a record whose status is not 0
+// are {-1, -1}. Frames are scanned in tiles of 8 per thread with one
+// block-wide prefix count per tile.
+__global__ void __launch_bounds__(256) spans_kernel(const ffa_span_record* recs, const int64_t* labels,
+                                                    const int32_t* status, int64_t* spans) {
+  __shared__ int wsum[4];
+  const ffa_span_record d = recs[blockIdx.x];
+  const GLB int64_t* lab = glb(labels) + d.frame_offset;
+  GLB int64_t* out = glb(spans) + 2 * d.span_offset;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (glb(status)[blockIdx.x] != 0) {
+    for (int64_t k = tid; k < 2 * (int64_t)d.tokens; k += blockDim.x) out[k] = -1;
+    return;
+  }
+  const int64_t T = d.frames;
+  const int64_t blank = d.blank;
+  int carry = 0;  // runs started before this tile
+  for (int64_t base = 0; base < T; base += 8 * (int64_t)blockDim.x) {
+    const int64_t f0 = base + 8 * (int64_t)tid;
+    int64_t x[10];  // frames f0-1 .. f0+8 (out-of-range frames read as blank)
+#pragma unroll
+    for (int q = 0; q < 10; ++q) {
+      const int64_t f = f0 - 1 + q;
+      x[q] = (f >= 0 && f < T) ? lab[f] : blank;
+    }
+    int starts = 0;
+#pragma unroll
+    for (int q = 1; q <= 8; ++q) starts += x[q] != blank && x[q] != x[q - 1];
+    // block-wide exclusive prefix of the run starts
+    int incl = wave_scan_dpp(starts);
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int before = carry;
+    for (int w = 0; w < wave; ++w) before += wsum[w];
+    int total = carry;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) total += wsum[w];
+    int k = before + incl - starts;  // index of the first run starting in this thread's frames
+#pragma unroll
+    for (int q = 1; q <= 8; ++q) {
+      const int64_t f = f0 - 1 + q;
+      const bool run = x[q] != blank;
+      if (run && x[q] != x[q - 1]) {  // run start
+        if (k < d.tokens) out[2 * k] = f;
+        ++k;
+      }
+      if (run && x[q + 1] != x[q] && k - 1 < d.tokens && k >= 1) out[2 * (k - 1) + 1] = f + 1;  // run end
+    }
+    __syncthreads();
+    carry = total;
+  }
+  // fewer runs than tokens (a transcript holding the blank id, unchecked): rows past the runs are -1
+  for (int64_t k = (int64_t)carry + tid; k < d.tokens; k += blockDim.x) { out[2 * k] = -1; out[2 * k + 1] = -1; }
+}
+
 // One workgroup per record: any NaN or +inf rejects it (cu:881-891).
 __global__ void __launch_bounds__(1024) validity_kernel(const int64_t* desc, uint8_t* valid) {
   const int rec = blockIdx.x;
@@ -2077,6 +2137,16 @@ extern "C" int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_opti
     case 32: return launch_geometry<32, 1>(p, NT, lds, optimized, stream);
     default: return fail(FFA_E_INVALID, "corrupt plan");
   }
+}
+
+extern "C" int ffa_token_spans_launch(const ffa_span_record* device_records, int64_t count, const int64_t* labels,
+                                      const int32_t* status, int64_t* spans, hipStream_t stream) {
+  if (count <= 0 || count > FFA_MAX_BATCH) return fail(FFA_E_INVALID, "provide 1..65535 records");
+  if (!device_records || !labels || !status || !spans) return fail(FFA_E_INVALID, "null record, label, status or span pointer");
+  hipLaunchKernelGGL(ffa::spans_kernel, dim3((unsigned)count), dim3(256), 0, stream, device_records, labels, status, spans);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(FFA_E_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
+  return FFA_OK;
 }
 
 extern "C" int ffa_emission_validity_launch(const int64_t* device_descriptors, int64_t count, uint8_t* valid,

@@ -297,6 +297,69 @@ py::tuple align_py(py::handle emissions, py::handle targets, py::handle blank_id
   return py::make_tuple(outs, lens);
 }
 
+// Token spans of an alignment's paths (ffa_token_spans_launch): labels and
+// status are align()'s outputs, lengths the frames and tokens the target
+// length of each record, blank_id an int or one int per record. Returns int64
+// [sum(tokens), 2] on the labels' device, enqueued on the current stream.
+py::object token_spans_py(py::handle labels_obj, py::handle status_obj, py::handle lengths_obj,
+                          py::handle tokens_obj, py::handle blank_id) {
+  c10::InferenceMode inference;
+  if (!THPVariable_Check(labels_obj.ptr()) || !THPVariable_Check(status_obj.ptr()))
+    throw py::value_error("labels and status must be tensors from align()");
+  const at::Tensor& labels = THPVariable_Unpack(labels_obj.ptr());
+  const at::Tensor& status = THPVariable_Unpack(status_obj.ptr());
+  py::object ls = py::reinterpret_steal<py::object>(PySequence_Fast(lengths_obj.ptr(), "lengths"));
+  py::object ts = py::reinterpret_steal<py::object>(PySequence_Fast(tokens_obj.ptr(), "tokens"));
+  if (!ls || !ts) throw py::error_already_set();
+  const int64_t count = PySequence_Fast_GET_SIZE(ls.ptr());
+  if (count <= 0 || count > FFA_MAX_BATCH || PySequence_Fast_GET_SIZE(ts.ptr()) != count)
+    throw py::value_error("provide one frame count and one target length per record");
+  if (!labels.is_cuda() || labels.scalar_type() != at::kLong || labels.dim() != 1 || !labels.is_contiguous() ||
+      status.device() != labels.device() || status.scalar_type() != at::kInt || status.dim() != 1 ||
+      status.numel() != count || !status.is_contiguous())
+    throw py::value_error("labels must be contiguous CUDA int64 [N] and status CUDA int32 [batch] from align()");
+  const bool uniform = PyLong_Check(blank_id.ptr()) && !PyBool_Check(blank_id.ptr());
+  py::object bs;
+  if (!uniform) {
+    bs = py::reinterpret_steal<py::object>(PySequence_Fast(blank_id.ptr(), "blank_id"));
+    if (!bs) throw py::error_already_set();
+    if (PySequence_Fast_GET_SIZE(bs.ptr()) != count) throw py::value_error("provide one blank ID per record");
+  }
+  const auto device = labels.device();
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(device);
+  const HIPStreamMasqueradingAsCUDA stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(device.index());
+  auto* host_alloc = at::getHostAllocator(at::kCUDA);
+  const int64_t table_bytes = count * (int64_t)sizeof(ffa_span_record);
+  c10::DataPtr host = host_alloc->allocate(table_bytes);
+  auto* recs = static_cast<ffa_span_record*>(host.get());
+  int64_t frame = 0, span = 0;
+  for (int64_t i = 0; i < count; ++i) {
+    const int64_t T = py::cast<int64_t>(PySequence_Fast_GET_ITEM(ls.ptr(), i));
+    const int64_t U = py::cast<int64_t>(PySequence_Fast_GET_ITEM(ts.ptr(), i));
+    const int64_t b = uniform ? py::cast<int64_t>(blank_id) : py::cast<int64_t>(PySequence_Fast_GET_ITEM(bs.ptr(), i));
+    if (T <= 0 || U < 0 || 2 * U + 1 > FFA_MAX_STATES || b < 0 || b >= FFA_MAX_VOCAB)
+      throw py::value_error("unsupported frame count, target length, or blank ID");
+    recs[i] = ffa_span_record{frame, T, span, (int32_t)U, (int32_t)b};
+    frame += T;
+    span += U;
+  }
+  if (frame != labels.numel()) throw py::value_error("frame counts do not add up to the labels' length");
+  recordStreamMasqueradingAsCUDA(labels.storage().data_ptr(), stream);
+  recordStreamMasqueradingAsCUDA(status.storage().data_ptr(), stream);
+  auto table = at::empty({align256(table_bytes)}, labels.options().dtype(at::kByte));
+  const hipError_t copied = hipMemcpyAsync(table.data_ptr(), host.get(), table_bytes, hipMemcpyHostToDevice,
+                                           stream.stream());
+  TORCH_CHECK(copied == hipSuccess, "fast_forced_aligner: span table upload failed: ", hipGetErrorString(copied));
+  host_alloc->record_event(host.get(), host.get_context(), stream.unwrap());
+  auto spans = at::empty({span, 2}, labels.options());
+  if (span > 0)
+    check_ffa(ffa_token_spans_launch(static_cast<const ffa_span_record*>(table.data_ptr()), count,
+                                     static_cast<const int64_t*>(labels.data_ptr()),
+                                     static_cast<const int32_t*>(status.data_ptr()),
+                                     static_cast<int64_t*>(spans.data_ptr()), stream.stream()));
+  return py::reinterpret_steal<py::object>(THPVariable_Wrap(spans));
+}
+
 }  // namespace
 
 TORCH_LIBRARY(fast_forced_aligner_cuda, m) {
@@ -317,4 +380,6 @@ PYBIND11_MODULE(_ffa_torch, m) {
   m.doc() = "MI355X CTC forced alignment: the package's direct entry to the HIP library";
   m.def("align", &align_py, py::arg("emissions"), py::arg("targets"), py::arg("blank_id"), py::arg("optimized"),
         py::arg("check_inputs"), py::arg("emission_validity"));
+  m.def("token_spans", &token_spans_py, py::arg("labels"), py::arg("status"), py::arg("lengths"),
+        py::arg("tokens"), py::arg("blank_id"));
 }

@@ -237,3 +237,47 @@ def align(emissions: Sequence[Tensor], targets: Sequence[Tensor], *,
     tensors, lengths = _native.align(emissions, targets, blank_id, mode == "optimized", check_inputs,
                                      emission_validity)
     return AlignmentBatch(lengths, *tensors)
+
+
+@dataclass(frozen=True)
+class TokenSpans:
+    """Token spans of an alignment: ``spans`` int64 ``(sum(lengths), 2)`` holds,
+    per record and in transcript order, the ``[start, end)`` frames of each
+    non-blank run of the path (``-1`` rows for records whose status is not 0);
+    ``lengths`` the target length of each record."""
+
+    lengths: tuple[int, ...]
+    spans: Tensor
+
+    def split(self) -> tuple[Tensor, ...]:
+        """Per-record ``(U_i, 2)`` views (no copy, no synchronization)."""
+        return self.spans.split(self.lengths)
+
+    def seconds(self, frame_stride: float) -> Tensor:
+        """Span boundaries in seconds: frames times the model's frame stride
+        (for Transformers CTC models ``inputs_to_logits_ratio / sample_rate``)."""
+        return self.spans.to(torch.float64) * frame_stride
+
+
+def token_spans(batch: AlignmentBatch, targets: Sequence[Tensor] | Sequence[int], *,
+                blank_id: int | Sequence[int] = 0) -> TokenSpans:
+    """Token spans of ``align``'s paths, computed on the GPU without a host sync.
+
+    Follows the reference README's "Converting frame labels to timestamps":
+    split each path into equal-label runs, discard blank runs, and keep each
+    remaining run's start and exclusive end frame; blank-separated repeated
+    tokens stay separate occurrences. A successful record has exactly one run
+    per target token.
+
+    Args:
+        batch: the result of ``align``.
+        targets: the targets passed to ``align`` (tensors) or their lengths.
+        blank_id: the blank id(s) passed to ``align``.
+
+    Raises:
+        ValueError: the batch, targets and blanks do not belong together.
+    """
+    tokens = [t if type(t) is int else int(t.numel()) for t in targets]
+    load_extension()
+    spans = _native.token_spans(batch.labels, batch.status, batch.lengths, tokens, blank_id)
+    return TokenSpans(tuple(tokens), spans)

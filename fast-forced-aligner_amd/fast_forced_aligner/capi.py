@@ -19,7 +19,12 @@ FFA_MAX_VOCAB = 8192
 FFA_MAX_STATES = 20479
 
 EXPORTED = ("ffa_default_options", "ffa_align_plan_batch", "ffa_align_describe", "ffa_align_launch",
-            "ffa_emission_validity_launch", "ffa_last_error", "ffa_profile_next_launch")
+            "ffa_emission_validity_launch", "ffa_token_spans_launch", "ffa_last_error", "ffa_profile_next_launch")
+
+
+class SpanRecord(ctypes.Structure):
+    _fields_ = [("frame_offset", ctypes.c_int64), ("frames", ctypes.c_int64), ("span_offset", ctypes.c_int64),
+                ("tokens", ctypes.c_int32), ("blank", ctypes.c_int32)]
 
 
 class Record(ctypes.Structure):
@@ -68,6 +73,8 @@ def load(path: Path | str = HIP_LIBRARY) -> ctypes.CDLL:
     lib.ffa_last_error.argtypes = []
     lib.ffa_profile_next_launch.restype = ctypes.c_int
     lib.ffa_profile_next_launch.argtypes = [p, p]
+    lib.ffa_token_spans_launch.restype = ctypes.c_int
+    lib.ffa_token_spans_launch.argtypes = [p, ctypes.c_int64, p, p, p, p]
     return lib
 
 

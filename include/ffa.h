@@ -126,6 +126,26 @@ int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_options* option
 int ffa_emission_validity_launch(const int64_t* device_descriptors, int64_t count, uint8_t* valid,
                                  hipStream_t stream);
 
+/* Token spans (the reference README's "Converting frame labels to timestamps",
+ * stated only in prose there; this entry has no native counterpart in the
+ * reference): for each record, the equal-label runs of its aligned path with
+ * blank runs removed, as [start, end) frame pairs. A successful record (status
+ * 0) has exactly `tokens` runs, written in order to spans[span_offset .. +tokens)
+ * as int64 {start, end}; multiply by the model's frame stride for timestamps.
+ * Records with a nonzero status get {-1, -1}. device_records: [count] records in
+ * device memory; labels / status: align()'s outputs; spans: int64
+ * [sum of tokens][2] in device memory. */
+typedef struct ffa_span_record {
+  int64_t frame_offset;  /* first frame of the record in labels */
+  int64_t frames;        /* T */
+  int64_t span_offset;   /* first span of the record */
+  int32_t tokens;        /* U: spans of a successful record */
+  int32_t blank;
+} ffa_span_record;
+
+int ffa_token_spans_launch(const ffa_span_record* device_records, int64_t count, const int64_t* labels,
+                           const int32_t* status, int64_t* spans, hipStream_t stream);
+
 /* Message for the last failing call on this thread. */
 const char* ffa_last_error(void);
 

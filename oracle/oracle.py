@@ -133,6 +133,30 @@ def emission_valid(emission: np.ndarray) -> bool:
     return bool(lib().orc_emission_valid(_ptr(e), e.size))
 
 
+def token_spans(labels: np.ndarray, lengths: Sequence[int], tokens: Sequence[int], status: np.ndarray,
+                blank_id=0) -> np.ndarray:
+    """Token spans of aligned paths, restating the reference README's
+    "Converting frame labels to timestamps" (README.md:509-517; no code in the
+    reference): split each path into equal-label runs, discard blank runs, keep
+    each remaining run's [start, end) frames. Rows per record = its target
+    length: records with nonzero status are all -1; missing runs are -1 and
+    extra runs are dropped (only possible for a transcript holding the blank id)."""
+    blanks = [blank_id] * len(lengths) if isinstance(blank_id, int) else list(blank_id)
+    out = np.full((int(sum(tokens)), 2), -1, dtype=np.int64)
+    frame = span = 0
+    for T, U, st, b in zip(lengths, tokens, status, blanks):
+        p = np.asarray(labels[frame:frame + T])
+        if st == 0 and U > 0:
+            edges = np.flatnonzero(np.r_[True, p[1:] != p[:-1]])
+            ends = np.r_[edges[1:], T]
+            keep = p[edges] != b
+            runs = np.stack([edges[keep], ends[keep]], axis=1)[:U]
+            out[span:span + len(runs)] = runs
+        frame += T
+        span += U
+    return out
+
+
 def reference_comparator():
     """The reference's own CPU comparator compiled into oracle/_ref, or None.
 
