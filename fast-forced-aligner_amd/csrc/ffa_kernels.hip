@@ -1823,11 +1823,17 @@ __global__ void __launch_bounds__(1024) validity_kernel(const int64_t* desc, uin
   }
   const GLB v4f_t* v4 = (const GLB v4f_t*)(values + head);
   const int64_t n4 = (n - head) / 4;
-  for (int64_t i = threadIdx.x; i < n4; i += blockDim.x) {
-    const v4f_t v = v4[i];
-    bad |= isnan(v.x) || v.x == INFINITY || isnan(v.y) || v.y == INFINITY ||
-           isnan(v.z) || v.z == INFINITY || isnan(v.w) || v.w == INFINITY;
+  auto reject = [](const v4f_t v) {  // NaN or +inf (x != x, or x == +inf)
+    return (v.x != v.x) | (v.x == INFINITY) | (v.y != v.y) | (v.y == INFINITY) | (v.z != v.z) | (v.z == INFINITY) |
+           (v.w != v.w) | (v.w == INFINITY);
+  };
+  const int64_t stride = blockDim.x;
+  int64_t i = threadIdx.x;
+  for (; i + 3 * stride < n4; i += 4 * stride) {  // four 16-byte loads in flight per thread
+    const v4f_t a = v4[i], b = v4[i + stride], c = v4[i + 2 * stride], d = v4[i + 3 * stride];
+    bad |= reject(a) | reject(b) | reject(c) | reject(d);
   }
+  for (; i < n4; i += stride) bad |= reject(v4[i]);
   for (int64_t i = head + 4 * n4 + threadIdx.x; i < n; i += blockDim.x) {
     const float v = values[i];
     bad |= isnan(v) || v == INFINITY;

@@ -297,6 +297,47 @@ py::tuple align_py(py::handle emissions, py::handle targets, py::handle blank_id
   return py::make_tuple(outs, lens);
 }
 
+// Python entry of the package's emission_validity() (alignment.cu:893-917):
+// the same scan as the operator, with the Python layer's per-record checks
+// (alignment.py:312-343) done here in C++ and the descriptors uploaded from a
+// caching-host-allocator block.
+py::object emission_validity_py(py::handle emissions) {
+  c10::InferenceMode inference;
+  py::object seq = py::reinterpret_steal<py::object>(PySequence_Fast(emissions.ptr(), "emissions"));
+  if (!seq) throw py::error_already_set();
+  const int64_t count = PySequence_Fast_GET_SIZE(seq.ptr());
+  if (count <= 0 || count > FFA_MAX_BATCH) throw py::value_error("provide 1..65535 emission tensors");
+  PyObject** items = PySequence_Fast_ITEMS(seq.ptr());
+  const char* bad = "emissions must be contiguous CUDA float32 [T,V] with supported dimensions on one device";
+  if (!THPVariable_Check(items[0]) || !THPVariable_Unpack(items[0]).is_cuda()) throw py::value_error(bad);
+  const auto device = THPVariable_Unpack(items[0]).device();
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(device);
+  const HIPStreamMasqueradingAsCUDA stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(device.index());
+  auto* host_alloc = at::getHostAllocator(at::kCUDA);
+  const int64_t bytes = 16 * count;
+  c10::DataPtr host = host_alloc->allocate(bytes);
+  auto* descriptors = static_cast<int64_t*>(host.get());
+  for (int64_t i = 0; i < count; ++i) {
+    if (!THPVariable_Check(items[i])) throw py::value_error(bad);
+    const at::Tensor& e = THPVariable_Unpack(items[i]);
+    if (!(e.is_cuda() && e.device() == device && e.scalar_type() == at::kFloat && e.dim() == 2 && e.is_contiguous() &&
+          e.size(0) > 0 && e.size(0) <= INT_MAX && e.size(1) > 0 && e.size(1) <= FFA_MAX_VOCAB))
+      throw py::value_error(bad);
+    descriptors[2 * i] = reinterpret_cast<int64_t>(e.data_ptr());
+    descriptors[2 * i + 1] = e.numel();
+    recordStreamMasqueradingAsCUDA(e.storage().data_ptr(), stream);
+  }
+  const auto options = THPVariable_Unpack(items[0]).options();
+  auto table = at::empty({align256(bytes)}, options.dtype(at::kByte));
+  const hipError_t copied = hipMemcpyAsync(table.data_ptr(), host.get(), bytes, hipMemcpyHostToDevice, stream.stream());
+  TORCH_CHECK(copied == hipSuccess, "fast_forced_aligner: descriptor upload failed: ", hipGetErrorString(copied));
+  host_alloc->record_event(host.get(), host.get_context(), stream.unwrap());
+  auto result = at::empty({count}, options.dtype(at::kBool));
+  check_ffa(ffa_emission_validity_launch(static_cast<const int64_t*>(table.data_ptr()), count,
+                                         reinterpret_cast<uint8_t*>(result.data_ptr()), stream.stream()));
+  return py::reinterpret_steal<py::object>(THPVariable_Wrap(result));
+}
+
 // Token spans of an alignment's paths (ffa_token_spans_launch): labels and
 // status are align()'s outputs, lengths the frames and tokens the target
 // length of each record, blank_id an int or one int per record. Returns int64
@@ -380,6 +421,7 @@ PYBIND11_MODULE(_ffa_torch, m) {
   m.doc() = "MI355X CTC forced alignment: the package's direct entry to the HIP library";
   m.def("align", &align_py, py::arg("emissions"), py::arg("targets"), py::arg("blank_id"), py::arg("optimized"),
         py::arg("check_inputs"), py::arg("emission_validity"));
+  m.def("emission_validity", &emission_validity_py, py::arg("emissions"));
   m.def("token_spans", &token_spans_py, py::arg("labels"), py::arg("status"), py::arg("lengths"),
         py::arg("tokens"), py::arg("blank_id"));
 }
