@@ -42,11 +42,13 @@ def hip_runtime():
     return lib
 
 
-def measure(ffa, capi_lib, hip, es, ys, mode, steps, warmup):
+def measure(capi_lib, hip, call, steps, warmup):
+    """Pipelined wall time per call of `call` (an align entry) and the average
+    duration of its dominant kernel from the armed HIP events."""
     import torch
 
     for _ in range(warmup):
-        ffa.align(es, ys, mode=mode)
+        call()
     torch.cuda.synchronize()
     starts, stops = [], []
     for _ in range(steps):
@@ -59,7 +61,7 @@ def measure(ffa, capi_lib, hip, es, ys, mode, steps, warmup):
     t0 = time.perf_counter()
     for i in range(steps):
         capi_lib.ffa_profile_next_launch(starts[i], stops[i])
-        result = ffa.align(es, ys, mode=mode)
+        result = call()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     kernel_ms = []
@@ -110,6 +112,50 @@ def extras(ffa, es, ys, result, steps=100):
                                   "GB_per_s": scan_bytes / t_scan / 1e9},
             "token_spans": {"us_per_call": t_spans * 1e6, "bytes": span_bytes,
                             "GB_per_s": span_bytes / t_spans / 1e9}}
+
+
+def logits_figures(ffa, capi_lib, hip, config, mode, steps=100):
+    """The fused logits path (align_logits) on the same config's raw logits,
+    beside the two unfused pipelines it replaces: torch's log_softmax per
+    record then align (the reference callers' pipeline,
+    examples/transformers_ctc/align.py:55-67), and this build's materialized
+    log_softmax then align. Bytes: every logit read once (the normalizer needs
+    the whole row), int64 label + fp32 score written per frame, targets read."""
+    import torch
+
+    from fast_forced_aligner import workloads
+
+    raw = workloads.make(config, raw=True)
+    xs = [torch.from_numpy(x).to("cuda:0") for x in raw.emissions]
+    ys = [torch.from_numpy(y).to("cuda:0") for y in raw.targets]
+    step_s, kernel_ms, fused = measure(capi_lib, hip, lambda: ffa.align_logits(xs, ys, mode=mode), steps, 10)
+    plain = ffa.align(ffa.log_softmax(xs), ys, mode=mode)
+
+    def bits(t):
+        return t.view(torch.int32) if t.dtype == torch.float32 else t
+
+    parity = all(torch.equal(bits(getattr(fused, f)), bits(getattr(plain, f)))
+                 for f in ("labels", "scores", "status", "objective"))
+
+    def timed(fn):
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps
+
+    t_torch = timed(lambda: ffa.align([x.log_softmax(-1) for x in xs], ys, mode=mode))
+    t_mat = timed(lambda: ffa.align(ffa.log_softmax(xs), ys, mode=mode))
+    nbytes = sum(4 * x.size + 12 * x.shape[0] for x in raw.emissions) + sum(8 * y.size for y in raw.targets)
+    achieved = nbytes / (kernel_ms * 1e-3) / 1e9
+    return {"workload": f"{config} raw logits, {mode} mode", "us_per_call": step_s * 1e6,
+            "frames_per_s": raw.frames / step_s, "kernel_us": kernel_ms * 1e3, "algorithmic_bytes": nbytes,
+            "roofline_frac": achieved / HBM_PEAK_GBS,
+            "torch_log_softmax_then_align_us": t_torch * 1e6, "log_softmax_then_align_us": t_mat * 1e6,
+            "parity_vs_materialized": bool(parity)}
 
 
 def cpu_baseline(batch, seconds=10.0):
@@ -170,7 +216,7 @@ def main() -> int:
     min_bytes = batch.min_bytes()
 
     def figures(mode, steps, warmup):
-        step_s, kernel_ms, result = measure(ffa, capi_lib, hip, es, ys, mode, steps, warmup)
+        step_s, kernel_ms, result = measure(capi_lib, hip, lambda: ffa.align(es, ys, mode=mode), steps, warmup)
         achieved = min_bytes / (kernel_ms * 1e-3) / 1e9
         return step_s, kernel_ms, achieved, result
 
@@ -211,6 +257,7 @@ def main() -> int:
                                 "dp_cells_per_s": batch.cells / c_step, "kernel_us": c_kernel_ms * 1e3,
                                 "roofline_frac": c_achieved / HBM_PEAK_GBS}
     line["extras"] = extras(ffa, es, ys, result)
+    line["extras"]["align_logits"] = logits_figures(ffa, capi_lib, hip, args.config, args.mode)
     line["cpu_baseline"] = None if args.no_cpu else cpu_baseline(batch)
     if args.calibrate_copy > 0:
         src = torch.ones(args.calibrate_copy << 18, dtype=torch.float32, device=dev)

@@ -103,6 +103,8 @@ struct Params {
   int32_t count, total_slots, H, mode, repair_rounds, check_inputs, overlap, frontier_batch;
   int32_t u_cap, d_cap, v_words, lds_tail_slots;
   int32_t eblk_frames;  // frames per LDS emission block of the DP (0: rows read straight from HBM)
+  int32_t logits;       // emissions are raw logits, aligned as their row log-softmax
+  float2* stats;        // logits: per frame {row max, log of the row's exp-sum}, indexed like labels
 };
 
 // ---------------------------------------------------------------------------
@@ -139,6 +141,7 @@ struct Lds {
   int16_t* sym;
   uint32_t* bitmap;
   uint32_t* wpref;
+  float2* st;      // logits: row statistics of the chunk's frames (chunk kernel)
   int32_t* cand;
   int32_t* candok;
   Slot* tslots;
@@ -175,6 +178,8 @@ __device__ inline Lds carve(unsigned char* base, const Params& p) {
   L.sym = reinterpret_cast<int16_t*>(region + g); g = align16(g + 2 * (size_t)p.d_cap);
   L.bitmap = reinterpret_cast<uint32_t*>(region + g); g += 4 * (size_t)p.v_words;
   L.wpref = reinterpret_cast<uint32_t*>(region + g);
+  g = align16(g + 4 * (size_t)p.v_words);
+  L.st = reinterpret_cast<float2*>(region + g);
   L.tslots = reinterpret_cast<Slot*>(region);
   return L;
 }
@@ -364,7 +369,97 @@ struct Rec {
   GLB int64_t* labels;  // this record's output rows
   GLB float* scores;
   const int16_t* ytok;
+  // Logits input: row statistics of frame t at st[t - st_first] (LDS in the
+  // chunk kernel, global memory elsewhere); nullptr for log-probabilities.
+  const float2* st;
+  int64_t st_first;
 };
+
+// Log-softmax of a raw logit from its row statistics: (x - max) - log(sum).
+__device__ inline float lsm(float x, float2 s) { return (x - s.x) - s.y; }
+
+typedef float v2f_t __attribute__((ext_vector_type(2)));
+__device__ inline void store_stats(GLB float2* dst, float2 v) { *(GLB v2f_t*)dst = v2f_t{v.x, v.y}; }
+
+// Row statistics of the logits input: m = the row's maximum (a zero maximum is
+// taken as +0.0) and ls = logf of the sum of expf(x - m), so that log_softmax
+// is lsm(x, {m, ls}), the formula of torch's log_softmax. The sum has one fixed
+// order shared by every routine below: lane l of a wave adds expf(x[l + 64k] - m)
+// for k = 0, 1, ... in turn, starting from +0.0, then the 64 lane sums combine
+// as s[l] += s[l + o] for o = 32, 16, 8, 4, 2, 1. A row of at most 32 values
+// held by one lane gives the same bits (lanes 32-63 would add +0.0, which
+// leaves every sum of exponentials unchanged).
+
+// One lane, a row of V <= 32 values in registers (x[c] for c >= V unused).
+__device__ __attribute__((always_inline)) inline float2 lane_row_stats(const float (&x)[32], int V) {
+  float t[16];
+#pragma unroll
+  for (int c = 0; c < 16; ++c) t[c] = fmaxf(2 * c < V ? x[2 * c] : NEG_INF, 2 * c + 1 < V ? x[2 * c + 1] : NEG_INF);
+#pragma unroll
+  for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+    for (int c = 0; c < w; ++c) t[c] = fmaxf(t[c], t[c + w]);
+  const float m = t[0] + 0.0f;
+  float e[32];
+#pragma unroll
+  for (int c = 0; c < 32; ++c) e[c] = c < V ? expf(x[c] - m) : 0.0f;
+#pragma unroll
+  for (int w = 16; w >= 1; w >>= 1)
+#pragma unroll
+    for (int c = 0; c < w; ++c) e[c] = e[c] + e[c + w];
+  return make_float2(m, logf(e[0]));
+}
+
+// R rows (rows_here <= R valid, stride V) by one wave; lane 0 returns the
+// statistics. The R rows' loads are interleaved to keep several in flight.
+template <int R>
+__device__ __attribute__((always_inline)) inline void wave_row_stats(const GLB float* row0, int rows_here, int V,
+                                                                      float2 (&out)[R]) {
+  const int lane = threadIdx.x & 63;
+  float m[R], sum[R];
+#pragma unroll
+  for (int q = 0; q < R; ++q) { m[q] = NEG_INF; sum[q] = 0.0f; }
+  for (int c = lane; c < V; c += 64)
+#pragma unroll
+    for (int q = 0; q < R; ++q)
+      if (q < rows_here) m[q] = fmaxf(m[q], row0[(int64_t)q * V + c]);
+#pragma unroll
+  for (int q = 0; q < R; ++q) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m[q] = fmaxf(m[q], __shfl_xor(m[q], off, 64));
+    m[q] = m[q] + 0.0f;
+  }
+  for (int c = lane; c < V; c += 64)
+#pragma unroll
+    for (int q = 0; q < R; ++q)
+      if (q < rows_here) sum[q] += expf(row0[(int64_t)q * V + c] - m[q]);
+#pragma unroll
+  for (int q = 0; q < R; ++q) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum[q] += __shfl_down(sum[q], off, 64);
+    out[q] = make_float2(m[q], logf(sum[q]));
+  }
+}
+
+// Statistics of n consecutive rows by the whole workgroup (waves take groups
+// of four rows); lane 0 of each wave writes them to lds_out and / or glb_out.
+__device__ __attribute__((always_inline)) inline void rows_stats(const GLB float* rows, int n, int V, float2* lds_out,
+                                                                  GLB float2* glb_out) {
+  constexpr int R = 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  for (int f0 = wave * R; f0 < n; f0 += nw * R) {
+    float2 st[R];
+    wave_row_stats<R>(rows + (int64_t)f0 * V, min(R, n - f0), V, st);
+    if (lane == 0) {
+#pragma unroll
+      for (int q = 0; q < R; ++q)
+        if (f0 + q < n) {
+          if (lds_out) lds_out[f0 + q] = st[q];
+          if (glb_out) store_stats(glb_out + f0 + q, st[q]);
+        }
+    }
+  }
+}
 
 __device__ inline Rec make_rec(const RecordDesc& d, const Params& p, const Lds& L) {
   Rec r;
@@ -381,6 +476,8 @@ __device__ inline Rec make_rec(const RecordDesc& d, const Params& p, const Lds& 
   r.labels = glb(p.labels) + d.frame_offset;
   r.scores = glb(p.scores) + d.frame_offset;
   r.ytok = L.ytok;
+  r.st = nullptr;  // set by kernels built for logits input
+  r.st_first = 0;
   return r;
 }
 
@@ -464,7 +561,8 @@ __device__ inline int trace_path(const Rec& r, int64_t a, int64_t b, int termina
       const int64_t tf = t - lane;
       const int lab = label_of(r, mine);
       r.labels[tf] = lab;
-      r.scores[tf] = r.e[tf * r.V + lab];
+      const float v = r.e[tf * r.V + lab];
+      r.scores[tf] = r.st ? lsm(v, r.st[tf - r.st_first]) : v;
     }
     t -= steps;
     s = cur;
@@ -472,7 +570,9 @@ __device__ inline int trace_path(const Rec& r, int64_t a, int64_t b, int termina
   return s;
 }
 
-template <int K, int D>
+// LG: logits input (emission reads pass through lsm with r.st); a template
+// parameter so that the log-probability build carries none of it.
+template <int K, int D, bool LG>
 __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const Lds& L, int64_t a, int64_t b, bool record_end,
                              const GLB float* resume_from, int64_t start_t, GLB float* save_frontier, int trace) {
   using Bits = typename BitsT<K>::type;
@@ -503,9 +603,11 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
     for (int k = 0; k < K; ++k) al[k] = (s0 + k < S) ? resume_from[s0 + k] : NEG_INF;
   } else {
     const GLB float* row = e + a * V;
+    const float2 st_a = LG ? r.st[a - r.st_first] : make_float2(0.0f, 0.0f);
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-      const float v = ldg_at(row, lab[k]);
+      float v = ldg_at(row, lab[k]);
+      if (LG) v = lsm(v, st_a);
       al[k] = (s0 + k < S && (a > 0 || s0 + k < 2)) ? v : NEG_INF;  // cu:409
     }
     if (active) store_row<K>(bp + a * (int64_t)r.stride, tid, (Bits)0);  // cu:410
@@ -574,12 +676,20 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
         if (idx < total) buf[i] = src[idx];
       }
     };
+    const float inv_v = 1.0f / (float)V;
     auto store_block = [&](int64_t tb, float* half) {
       const int total = (int)(min(tb + F, b) - tb) * (int)V;
 #pragma unroll
       for (int i = 0; i < EB; ++i) {
         const int idx = tid + i * NT;
-        if (idx < total) half[idx] = buf[i];
+        if (idx < total) {
+          float v = buf[i];
+          if (LG) {  // frame of element idx: idx / V, exact in fp32 for idx < F * V <= 2048
+            const int f = (int)(((float)idx + 0.5f) * inv_v);
+            v = lsm(v, r.st[tb + f - r.st_first]);
+          }
+          half[idx] = v;
+        }
       }
     };
     int half = 0;
@@ -609,26 +719,43 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
   // the interval are clamped to its last row so every load is unconditional.
   // The main loop runs whole groups of D frames with no exits inside a group.
   float ev[D][K];
+  // logits: the row statistics travel with the gathers and are applied when
+  // the frame is computed
+  float2 es[D];
 #pragma unroll
   for (int d = 0; d < D; ++d) {
-    const GLB float* row = e + min(start_t + d, last) * V;
+    const int64_t t = min(start_t + d, last);
+    const GLB float* row = e + t * V;
 #pragma unroll
     for (int k = 0; k < K; ++k) ev[d][k] = ldg_at(row, lab[k]);
+    es[d] = LG ? r.st[t - r.st_first] : make_float2(0.0f, 0.0f);
   }
+  auto apply = [&](float (&evk)[K], float2 st) {
+    if (LG) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) evk[k] = lsm(evk[k], st);
+    }
+  };
   int64_t t0 = start_t;
   for (; t0 + D <= b; t0 += D) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
+      apply(ev[d], es[d]);
       frame(t0 + d, ev[d]);
-      const GLB float* row = e + min(t0 + d + D, last) * V;
+      const int64_t t = min(t0 + d + D, last);
+      const GLB float* row = e + t * V;
 #pragma unroll
       for (int k = 0; k < K; ++k) ev[d][k] = ldg_at(row, lab[k]);
+      if (LG) es[d] = r.st[t - r.st_first];
     }
   }
   // remaining < D frames: their gathers are already in ev[0 .. b-t0-1]
 #pragma unroll
   for (int d = 0; d < D; ++d)
-    if (t0 + d < b) frame(t0 + d, ev[d]);
+    if (t0 + d < b) {
+      apply(ev[d], es[d]);
+      frame(t0 + d, ev[d]);
+    }
   }
   if (save_frontier) {  // cu:451-454
 #pragma unroll
@@ -906,6 +1033,7 @@ __device__ __attribute__((always_inline)) int greedy_chunk(const Rec& r, const L
     __syncthreads();
     for (int f = tid; f < n; f += NT) {
       const GLB float* row = r.e + (a + f) * (int64_t)V;
+      const float2 st_f = r.st ? r.st[a + f - r.st_first] : make_float2(0.0f, 0.0f);
       float best = NEG_INF;
       int chosen = -1;
       bool dup = false;
@@ -916,6 +1044,10 @@ __device__ __attribute__((always_inline)) int greedy_chunk(const Rec& r, const L
         for (int q = 0; q < 8; ++q) {
           c[q] = L.sym[min(base + q, D - 1)];
           v[q] = ldg_at(row, 4u * (uint32_t)c[q]);
+        }
+        if (r.st) {
+#pragma unroll
+          for (int q = 0; q < 8; ++q) v[q] = lsm(v[q], st_f);
         }
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
@@ -1297,13 +1429,14 @@ __device__ __attribute__((always_inline)) int greedy_fast(const Lds& L, const fl
 // ---------------------------------------------------------------------------
 // Kernels.
 
-template <int K, int D>
+template <int K, int D, bool LG>
 __global__ void __launch_bounds__(K == 32 ? 640 : 256) conventional_kernel(Params p) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   const Lds L = carve(lds_raw, p);
   const int rec = blockIdx.x;
   const RecordDesc d = load_pod(glb(p.desc) + rec);
   Rec r = make_rec(d, p, L);
+  if (LG) r.st = p.stats + d.frame_offset;
   const Staged st = stage_tokens(d, p, rec, L, ALPHABET_NONE);
   if (threadIdx.x == 0) {
     glb(p.stitched)[rec] = 0;
@@ -1316,7 +1449,7 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) conventional_kernel(Param
     write_failed(r, 0, r.T);
     return;
   }
-  const DPOut o = dp_interval<K, D>(r, L, 0, r.T, true, nullptr, 1, nullptr, TRACE_IF_FINITE);
+  const DPOut o = dp_interval<K, D, LG>(r, L, 0, r.T, true, nullptr, 1, nullptr, TRACE_IF_FINITE);
   const bool ok = isfinite(o.score);
   if (threadIdx.x == 0) { glb(p.status)[rec] = ok ? 0 : 1; glb(p.objective)[rec] = o.score; }  // cu:507-510
   if (!ok) write_failed(r, 0, r.T);
@@ -1337,7 +1470,7 @@ __device__ inline Slot load_slot(const Slot* x) { return *x; }
 __device__ inline Slot load_slot(const GLB Slot* x) { return load_pod(x); }
 
 // The tail of one record; SP is the slot array, in LDS or in global memory.
-template <int K, int D, class SP>
+template <int K, int D, bool LG, class SP>
 __device__ __attribute__((always_inline)) void tail_body(const Params& p, const RecordDesc& d, int rec, const Rec& r,
                                                       const Lds& L, SP sl, bool in_lds) {
   Header* h = L.h;
@@ -1483,7 +1616,7 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
         const Slot s0 = load_slot(sl + (0));
         const bool resume = frontier_on && s0.frontier_end > 0 && s0.frontier_end <= T;
         if (resume) { reuse1 += s0.frontier_end; reuse3 += S; }
-        const DPOut o = dp_interval<K, D>(r, L, 0, T, true, resume ? r.frontier : nullptr,
+        const DPOut o = dp_interval<K, D, LG>(r, L, 0, T, true, resume ? r.frontier : nullptr,
                                           resume ? s0.frontier_end : 1, nullptr, TRACE_IF_FINITE);
         status = isfinite(o.score) ? 0 : 1;
         objective = o.score;
@@ -1507,7 +1640,7 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
           }
           reuse2 += S;
         }
-        const DPOut o = dp_interval<K, D>(r, L, s.a, s.b, s.b == T, resume ? fr : nullptr, start_t, fr,
+        const DPOut o = dp_interval<K, D, LG>(r, L, s.a, s.b, s.b == T, resume ? fr : nullptr, start_t, fr,
                                           TRACE_ALWAYS);
         if (tid == 0) {
           sl[k].objective = o.score;
@@ -1547,7 +1680,7 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
       const Slot s0 = load_slot(sl + (0));
       const bool resume = frontier_on && s0.frontier_end > 0 && s0.frontier_end <= T;
       if (resume) { reuse1 += s0.frontier_end; reuse3 += S; }
-      const DPOut o = dp_interval<K, D>(r, L, 0, T, true, resume ? r.frontier : nullptr,
+      const DPOut o = dp_interval<K, D, LG>(r, L, 0, T, true, resume ? r.frontier : nullptr,
                                         resume ? s0.frontier_end : 1, nullptr, TRACE_IF_FINITE);
       status = isfinite(o.score) ? 0 : 1;
       objective = o.score;
@@ -1577,7 +1710,7 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
 // stages and validates the record's targets, takes the greedy shortcut
 // (cu:30-153) or runs the relaxed chunk DP (cu:721-726), and writes the
 // chunk's labels, scores and slot.
-template <int K, int D>
+template <int K, int D, bool LG>
 __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   const Lds L = carve(lds_raw, p);
@@ -1595,8 +1728,8 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
   float x[32];
 #pragma unroll
   for (int q = 0; q < 32; ++q) x[q] = NEG_INF;
+  const int quads = (int)((ce.word >> 25) & 7u) + 1;  // V / 4 (fast path)
   if (fast && tid < n) {
-    const int quads = (int)((ce.word >> 25) & 7u) + 1;  // V / 4
     const GLB v4f_t* src = (const GLB v4f_t*)glb(ce.rows) + (int64_t)tid * quads;
 #pragma unroll
     for (int q = 0; q < 8; ++q)
@@ -1606,8 +1739,26 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
       }
   }
   const RecordDesc d = load_uniform(p.desc + rec);
+  // logits, fast path: each lane normalizes its own row in registers while the
+  // descriptor is in flight
+  float2 row_st = make_float2(0.0f, 0.0f);
+  if (LG && fast && tid < n) {
+    row_st = lane_row_stats(x, 4 * quads);
+#pragma unroll
+    for (int c = 0; c < 32; ++c)
+      if (c < 4 * quads) x[c] = lsm(x[c], row_st);
+    L.st[tid] = row_st;
+  }
   const Staged st = stage_targets(glb(d.targets), d.tokens, d.vocab, d.blank, d.frames, rec, p, L,
                                   p.mode != 2 ? ALPHABET_NONE : (fast ? ALPHABET_MASK32 : ALPHABET_BITMAP), fast);
+  if (LG) {  // the tail kernel's DP reads the statistics from global memory
+    if (fast) {
+      if (tid < n) store_stats(glb(p.stats) + d.frame_offset + a + tid, row_st);
+    } else if (st.status < 2) {
+      rows_stats(glb(d.emissions) + a * (int64_t)d.vocab, n, d.vocab, L.st, glb(p.stats) + d.frame_offset + a);
+      __syncthreads();
+    }
+  }
   Slot out{};
   out.a = (int)a;
   out.b = (int)b;
@@ -1632,11 +1783,12 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
       }
     }
     if (!accepted) {
-      const Rec r = make_rec(d, p, L);
+      Rec r = make_rec(d, p, L);
+      if (LG) { r.st = L.st; r.st_first = a; }
       if (p.mode == 2 && !fast) accepted = greedy_chunk(r, L, a, b, st.blank_in, out, &ambiguous);
       if (!accepted) {  // initial chunk DP (cu:721-726), relaxed init for a > 0
         GLB float* fr = r.frontier ? r.frontier + (int64_t)ce.chunk * r.S : nullptr;
-        const DPOut o = dp_interval<K, D>(r, L, a, b, b == r.T, nullptr, a + 1, fr, TRACE_ALWAYS);
+        const DPOut o = dp_interval<K, D, LG>(r, L, a, b, b == r.T, nullptr, a + 1, fr, TRACE_ALWAYS);
         out.objective = o.score;
         out.end = o.terminal;
         out.start = o.start;
@@ -1664,7 +1816,7 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
 // every neighbour and its budget preflight proposes no region) and
 // validate_seams stitches iff the fp32 total is finite. Wave 0 checks all
 // seams at once from registers and writes the record's outputs.
-template <int K, int D>
+template <int K, int D, bool LG>
 __global__ void __launch_bounds__(K == 32 ? 640 : 256) tail_kernel(Params p) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   const Lds L = carve(lds_raw, p);
@@ -1737,14 +1889,15 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) tail_kernel(Params p) {
     if (h->last) return;
     __syncthreads();
   }
-  const Rec r = make_rec(d, p, L);
+  Rec r = make_rec(d, p, L);
+  if (LG) r.st = p.stats + d.frame_offset;
   if (n <= p.lds_tail_slots) {
     Slot* ls = reinterpret_cast<Slot*>(lds_raw + ((uintptr_t)L.tslots - (uintptr_t)lds_raw));
     for (int k = tid; k < n; k += blockDim.x) ls[k] = load_pod(gs + k);
     __syncthreads();
-    tail_body<K, D>(p, d, rec, r, L, ls, true);
+    tail_body<K, D, LG>(p, d, rec, r, L, ls, true);
   } else {
-    tail_body<K, D>(p, d, rec, r, L, gs, false);
+    tail_body<K, D, LG>(p, d, rec, r, L, gs, false);
   }
 }
 
@@ -1809,6 +1962,34 @@ __global__ void __launch_bounds__(256) spans_kernel(const ffa_span_record* recs,
 }
 
 // One workgroup per record: any NaN or +inf rejects it (cu:881-891).
+// Conventional mode with logits input: the row statistics of every frame,
+// one workgroup per 128 frames of a record (grid: frame groups x records),
+// before the full-record DP reads them.
+__global__ void __launch_bounds__(256) stats_kernel(Params p) {
+  const RecordDesc d = load_uniform(p.desc + blockIdx.y);
+  const int64_t a = (int64_t)blockIdx.x * 128;
+  if (a >= d.frames) return;
+  const int n = (int)min((int64_t)128, d.frames - a);
+  rows_stats(glb(d.emissions) + a * (int64_t)d.vocab, n, d.vocab, nullptr, glb(p.stats) + d.frame_offset + a);
+}
+
+// Materialized log-softmax with the same row statistics as the fused path:
+// out = (x - m) - ls per element, 128 frames of one record per workgroup.
+__global__ void __launch_bounds__(256) log_softmax_kernel(const ffa_logits_record* recs) {
+  __shared__ float2 st[128];
+  const ffa_logits_record d = load_uniform(recs + blockIdx.y);
+  const int64_t a = (int64_t)blockIdx.x * 128;
+  if (a >= d.frames) return;
+  const int n = (int)min((int64_t)128, d.frames - a);
+  const int V = (int)d.vocab;
+  const GLB float* src = glb(d.logits) + a * V;
+  GLB float* dst = glb(d.log_probs) + a * V;
+  rows_stats(src, n, V, st, nullptr);
+  __syncthreads();
+  const int total = n * V;
+  for (int i = threadIdx.x; i < total; i += blockDim.x) dst[i] = lsm(src[i], st[i / V]);
+}
+
 __global__ void __launch_bounds__(1024) validity_kernel(const int64_t* desc, uint8_t* valid) {
   const int rec = blockIdx.x;
   const GLB float* values = (const GLB float*)(glb(desc)[2 * rec]);
@@ -1861,22 +2042,26 @@ inline int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 // internal[] of ffa_align_plan
 enum {
   I_K, I_NT, I_SLOTS, I_LDS, I_UCAP, I_DCAP, I_VWORDS, I_TAILSLOTS, I_FRONTIER, I_BUDGET,
-  I_OVERLAP, I_WS_SLOTS, I_WS_FRONTIER, I_MODE, I_H, I_FMIN, I_REPAIR_MIN, I_EBLK
+  I_OVERLAP, I_WS_SLOTS, I_WS_FRONTIER, I_MODE, I_H, I_FMIN, I_REPAIR_MIN, I_EBLK, I_LOGITS, I_WS_STATS,
+  I_MAX_FRAMES
 };
 
-template <int K, int D>
-int launch_geometry(const ffa::Params& p, int NT, size_t lds, bool optimized, hipStream_t stream) {
+template <int K, int D, bool LG>
+int launch_geometry(const ffa::Params& p, int NT, size_t lds, bool optimized, int64_t max_frames, hipStream_t stream) {
   hipEvent_t start = g_profile_start, stop = g_profile_stop;
   g_profile_start = g_profile_stop = nullptr;
+  if (p.logits && !optimized)
+    hipLaunchKernelGGL(ffa::stats_kernel, dim3((unsigned)((max_frames + 127) / 128), (unsigned)p.count), dim3(256), 0,
+                       stream, p);
   if (start) (void)hipEventRecord(start, stream);
   if (!optimized) {
-    hipLaunchKernelGGL((ffa::conventional_kernel<K, D>), dim3(p.count), dim3(NT), lds, stream, p);
+    hipLaunchKernelGGL((ffa::conventional_kernel<K, D, LG>), dim3(p.count), dim3(NT), lds, stream, p);
   } else {
     const int grid = 8 * ((p.total_slots + 7) / 8);
-    hipLaunchKernelGGL((ffa::chunk_kernel<K, D>), dim3(grid), dim3(std::max(NT, 128)), lds, stream, p);
+    hipLaunchKernelGGL((ffa::chunk_kernel<K, D, LG>), dim3(grid), dim3(std::max(NT, 128)), lds, stream, p);
   }
   if (stop) (void)hipEventRecord(stop, stream);
-  if (optimized) hipLaunchKernelGGL((ffa::tail_kernel<K, D>), dim3(p.count), dim3(NT), lds, stream, p);
+  if (optimized) hipLaunchKernelGGL((ffa::tail_kernel<K, D, LG>), dim3(p.count), dim3(NT), lds, stream, p);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(FFA_E_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
   return FFA_OK;
@@ -1953,6 +2138,8 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
     return fail(FFA_E_INVALID, "batch must contain 1..65535 matching emissions, targets and blanks");
   if (o->chunk_frames <= 0 || o->chunk_frames > MAX_H || o->mode < 0 || o->mode > 2)
     return fail(FFA_E_INVALID, "invalid chunk size or mode (chunk_frames must be 1..512)");
+  if (o->logits != 0 && o->logits != 1) return fail(FFA_E_INVALID, "logits must be 0 or 1");
+  const bool logits = o->logits != 0;
   const bool optimized = o->mode != 0;
   const int64_t H = o->chunk_frames;
   int64_t total_frames = 0, bp_words = 0, slots = 0, frontier_floats = 0;
@@ -1992,7 +2179,8 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
   geometry(s_max, &K, &NT);
   const int64_t v_words = (v_max + 31) / 32;
   const int64_t tail_slots = optimized ? std::min<int64_t>(n_max, ffa::TAIL_SLOT_CAP) : 0;
-  const int64_t greedy_bytes = 20 * ffa::greedy_frames(H) + 2048 + align_up(2 * d_cap, 16) + 8 * v_words;
+  const int64_t greedy_bytes = 20 * ffa::greedy_frames(H) + 2048 + align_up(2 * d_cap, 16) + 8 * v_words +
+                               (logits ? 16 + 8 * ffa::greedy_frames(H) : 0);
   const int64_t region = std::max(greedy_bytes, 32 * tail_slots);
   const int64_t targets = align_up(2 * (std::max<int64_t>(u_max, 1) + ffa::YTOK_PAD), 16);
   int64_t lds = align_up((int64_t)sizeof(ffa::Header), 16) + 2 * targets + region;
@@ -2009,6 +2197,8 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
   ws += align_up(32 * slots, 256);
   const int64_t ws_frontier = ws;
   ws += align_up(4 * frontier_floats, 256);
+  const int64_t ws_stats = ws;
+  if (logits) ws += align_up(8 * total_frames, 256);
   std::memset(plan, 0, sizeof(*plan));
   plan->count = count;
   plan->total_frames = total_frames;
@@ -2034,6 +2224,9 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
   in[I_H] = H;
   in[I_FMIN] = o->frontier_min_frames;
   in[I_REPAIR_MIN] = o->repair_min_frames;
+  in[I_LOGITS] = logits ? 1 : 0;
+  in[I_WS_STATS] = ws_stats;
+  in[I_MAX_FRAMES] = max_frames;
   return FFA_OK;
 }
 
@@ -2099,7 +2292,8 @@ extern "C" int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_opti
       !out->stitched || !out->repair_passes || !out->repaired_frames || !out->shortcut_stats || !out->routing_stats)
     return fail(FFA_E_INVALID, "null table, workspace or output pointer");
   if (plan->reuse_rows > 0 && !out->reuse_stats) return fail(FFA_E_INVALID, "reuse_stats required for this plan");
-  if (o->mode != in[I_MODE] || o->chunk_frames != in[I_H]) return fail(FFA_E_INVALID, "options differ from the plan");
+  if (o->mode != in[I_MODE] || o->chunk_frames != in[I_H] || (o->logits != 0) != (in[I_LOGITS] != 0))
+    return fail(FFA_E_INVALID, "options differ from the plan");
   ffa::Params p{};
   p.desc = static_cast<const ffa::RecordDesc*>(device_table);
   p.chunks = reinterpret_cast<const ffa::ChunkEntry*>(p.desc + plan->count);
@@ -2134,13 +2328,19 @@ extern "C" int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_opti
   p.v_words = (int32_t)in[I_VWORDS];
   p.lds_tail_slots = (int32_t)in[I_TAILSLOTS];
   p.eblk_frames = (int32_t)in[I_EBLK];
+  p.logits = (int32_t)in[I_LOGITS];
+  p.stats = p.logits ? reinterpret_cast<float2*>(ws + in[I_WS_STATS]) : nullptr;
   const int NT = (int)in[I_NT];
   const size_t lds = (size_t)in[I_LDS];
   switch (in[I_K]) {
-    case 4: return launch_geometry<4, 8>(p, NT, lds, optimized, stream);
-    case 8: return launch_geometry<8, 6>(p, NT, lds, optimized, stream);
-    case 16: return launch_geometry<16, 4>(p, NT, lds, optimized, stream);
-    case 32: return launch_geometry<32, 1>(p, NT, lds, optimized, stream);
+    case 4: return p.logits ? launch_geometry<4, 8, true>(p, NT, lds, optimized, in[I_MAX_FRAMES], stream)
+                      : launch_geometry<4, 8, false>(p, NT, lds, optimized, in[I_MAX_FRAMES], stream);
+    case 8: return p.logits ? launch_geometry<8, 6, true>(p, NT, lds, optimized, in[I_MAX_FRAMES], stream)
+                      : launch_geometry<8, 6, false>(p, NT, lds, optimized, in[I_MAX_FRAMES], stream);
+    case 16: return p.logits ? launch_geometry<16, 4, true>(p, NT, lds, optimized, in[I_MAX_FRAMES], stream)
+                      : launch_geometry<16, 4, false>(p, NT, lds, optimized, in[I_MAX_FRAMES], stream);
+    case 32: return p.logits ? launch_geometry<32, 1, true>(p, NT, lds, optimized, in[I_MAX_FRAMES], stream)
+                      : launch_geometry<32, 1, false>(p, NT, lds, optimized, in[I_MAX_FRAMES], stream);
     default: return fail(FFA_E_INVALID, "corrupt plan");
   }
 }
@@ -2150,6 +2350,18 @@ extern "C" int ffa_token_spans_launch(const ffa_span_record* device_records, int
   if (count <= 0 || count > FFA_MAX_BATCH) return fail(FFA_E_INVALID, "provide 1..65535 records");
   if (!device_records || !labels || !status || !spans) return fail(FFA_E_INVALID, "null record, label, status or span pointer");
   hipLaunchKernelGGL(ffa::spans_kernel, dim3((unsigned)count), dim3(256), 0, stream, device_records, labels, status, spans);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(FFA_E_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
+  return FFA_OK;
+}
+
+extern "C" int ffa_log_softmax_launch(const ffa_logits_record* device_records, int64_t count, int64_t max_frames,
+                                      hipStream_t stream) {
+  if (count <= 0 || count > FFA_MAX_BATCH) return fail(FFA_E_INVALID, "provide 1..65535 records");
+  if (max_frames <= 0 || max_frames > INT_MAX) return fail(FFA_E_INVALID, "max_frames must be 1..2^31-1");
+  if (!device_records) return fail(FFA_E_INVALID, "null record pointer");
+  hipLaunchKernelGGL(ffa::log_softmax_kernel, dim3((unsigned)((max_frames + 127) / 128), (unsigned)count), dim3(256),
+                     0, stream, device_records);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(FFA_E_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
   return FFA_OK;

@@ -23,6 +23,7 @@
 #include <torch/library.h>
 #include <pybind11/pybind11.h>
 
+#include <algorithm>
 #include <climits>
 #include <optional>
 #include <tuple>
@@ -228,7 +229,7 @@ std::tuple<std::vector<at::Tensor>, std::vector<int64_t>> align_op(
 // tensors and the record lengths. Outputs are inference tensors, as under the
 // reference's @torch.inference_mode.
 py::tuple align_py(py::handle emissions, py::handle targets, py::handle blank_id, bool optimized,
-                   bool check_inputs, py::handle validity) {
+                   bool check_inputs, py::handle validity, bool logits) {
   c10::InferenceMode inference;
   py::object es_seq = py::reinterpret_steal<py::object>(PySequence_Fast(emissions.ptr(), "emissions"));
   py::object ys_seq = py::reinterpret_steal<py::object>(PySequence_Fast(targets.ptr(), "targets"));
@@ -276,6 +277,7 @@ py::tuple align_py(py::handle emissions, py::handle targets, py::handle blank_id
   ffa_align_options o;
   ffa_default_options(optimized ? 1 : 0, &o);
   o.check_inputs = check_inputs;
+  o.logits = logits ? 1 : 0;
   std::tuple<std::vector<at::Tensor>, std::vector<int64_t>> result;
   try {
     result = run_align(
@@ -336,6 +338,60 @@ py::object emission_validity_py(py::handle emissions) {
   check_ffa(ffa_emission_validity_launch(static_cast<const int64_t*>(table.data_ptr()), count,
                                          reinterpret_cast<uint8_t*>(result.data_ptr()), stream.stream()));
   return py::reinterpret_steal<py::object>(THPVariable_Wrap(result));
+}
+
+// Row log-softmax of raw logits (ffa_log_softmax_launch): the values the
+// fused logits path of align() works on, materialized. `logits` is a sequence
+// of contiguous CUDA float32 [T, V] tensors on one device; returns one tensor
+// per record, views of one allocation, enqueued on the current stream.
+py::list log_softmax_py(py::handle logits_obj) {
+  c10::InferenceMode inference;
+  py::object seq = py::reinterpret_steal<py::object>(PySequence_Fast(logits_obj.ptr(), "logits"));
+  if (!seq) throw py::error_already_set();
+  const int64_t count = PySequence_Fast_GET_SIZE(seq.ptr());
+  if (count <= 0 || count > FFA_MAX_BATCH) throw py::value_error("provide 1..65535 logit tensors");
+  PyObject** items = PySequence_Fast_ITEMS(seq.ptr());
+  const char* bad = "logits must be contiguous CUDA float32 [T,V] with supported dimensions on one device";
+  if (!THPVariable_Check(items[0]) || !THPVariable_Unpack(items[0]).is_cuda()) throw py::value_error(bad);
+  const auto device = THPVariable_Unpack(items[0]).device();
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(device);
+  const HIPStreamMasqueradingAsCUDA stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(device.index());
+  std::vector<int64_t> offsets(count);
+  int64_t total = 0, max_frames = 0;
+  for (int64_t i = 0; i < count; ++i) {
+    if (!THPVariable_Check(items[i])) throw py::value_error(bad);
+    const at::Tensor& x = THPVariable_Unpack(items[i]);
+    if (!(x.is_cuda() && x.device() == device && x.scalar_type() == at::kFloat && x.dim() == 2 && x.is_contiguous() &&
+          x.size(0) > 0 && x.size(0) <= INT_MAX && x.size(1) > 0 && x.size(1) <= FFA_MAX_VOCAB))
+      throw py::value_error(bad);
+    offsets[i] = total;
+    total += align256(4 * x.numel());
+    max_frames = std::max<int64_t>(max_frames, x.size(0));
+  }
+  const auto options = THPVariable_Unpack(items[0]).options();
+  auto block = at::empty({total}, options.dtype(at::kByte));
+  auto* base = static_cast<uint8_t*>(block.data_ptr());
+  auto* host_alloc = at::getHostAllocator(at::kCUDA);
+  const int64_t table_bytes = count * (int64_t)sizeof(ffa_logits_record);
+  c10::DataPtr host = host_alloc->allocate(table_bytes);
+  auto* recs = static_cast<ffa_logits_record*>(host.get());
+  py::list outs(count);
+  for (int64_t i = 0; i < count; ++i) {
+    const at::Tensor& x = THPVariable_Unpack(items[i]);
+    recs[i] = ffa_logits_record{static_cast<const float*>(x.data_ptr()), reinterpret_cast<float*>(base + offsets[i]),
+                                x.size(0), x.size(1)};
+    recordStreamMasqueradingAsCUDA(x.storage().data_ptr(), stream);
+    outs[i] = py::reinterpret_steal<py::object>(
+        THPVariable_Wrap(view_of(block, offsets[i], at::kFloat, {x.size(0), x.size(1)})));
+  }
+  auto table = at::empty({align256(table_bytes)}, options.dtype(at::kByte));
+  const hipError_t copied = hipMemcpyAsync(table.data_ptr(), host.get(), table_bytes, hipMemcpyHostToDevice,
+                                           stream.stream());
+  TORCH_CHECK(copied == hipSuccess, "fast_forced_aligner: record table upload failed: ", hipGetErrorString(copied));
+  host_alloc->record_event(host.get(), host.get_context(), stream.unwrap());
+  check_ffa(ffa_log_softmax_launch(static_cast<const ffa_logits_record*>(table.data_ptr()), count, max_frames,
+                                   stream.stream()));
+  return outs;
 }
 
 // Token spans of an alignment's paths (ffa_token_spans_launch): labels and
@@ -420,7 +476,8 @@ TORCH_LIBRARY_IMPL(fast_forced_aligner_cuda, CUDA, m) {
 PYBIND11_MODULE(_ffa_torch, m) {
   m.doc() = "MI355X CTC forced alignment: the package's direct entry to the HIP library";
   m.def("align", &align_py, py::arg("emissions"), py::arg("targets"), py::arg("blank_id"), py::arg("optimized"),
-        py::arg("check_inputs"), py::arg("emission_validity"));
+        py::arg("check_inputs"), py::arg("emission_validity"), py::arg("logits") = false);
+  m.def("log_softmax", &log_softmax_py, py::arg("logits"));
   m.def("emission_validity", &emission_validity_py, py::arg("emissions"));
   m.def("token_spans", &token_spans_py, py::arg("labels"), py::arg("status"), py::arg("lengths"),
         py::arg("tokens"), py::arg("blank_id"));

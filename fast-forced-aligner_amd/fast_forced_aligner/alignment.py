@@ -235,6 +235,48 @@ def align(emissions: Sequence[Tensor], targets: Sequence[Tensor], *,
     return AlignmentBatch(lengths, *tensors)
 
 
+def align_logits(logits: Sequence[Tensor], targets: Sequence[Tensor], *,
+                 blank_id: int | Sequence[int] = 0, mode: Mode = "optimized",
+                 check_inputs: bool = True, emission_validity: Tensor | None = None) -> AlignmentBatch:
+    """``align`` on raw logits, with the row log-softmax fused into the kernels.
+
+    The producer step of the reference's callers
+    (examples/transformers_ctc/align.py:55-56, ``logits.float().log_softmax(-1)``)
+    moves inside the alignment: each frame's log-softmax is computed where the
+    row is read, so the normalized ``(T, V)`` tensors are never written or read
+    back. The result equals ``align(log_softmax(logits), ...)`` bit for bit
+    (``log_softmax`` below materializes the same values); ``scores`` are those
+    log-probabilities. Same arguments, statuses and exceptions as ``align``,
+    with ``logits`` in place of ``emissions``.
+    """
+    if mode not in ("optimized", "conventional"):
+        raise ValueError("mode must be 'optimized' or 'conventional'")
+    if type(check_inputs) is not bool:
+        raise TypeError("check_inputs must be bool")
+    if not (logits and isinstance(logits[0], Tensor) and logits[0].is_cuda):
+        _metadata(logits, targets, blank_id)
+    load_extension()
+    tensors, lengths = _native.align(logits, targets, blank_id, mode == "optimized", check_inputs,
+                                     emission_validity, True)
+    return AlignmentBatch(lengths, *tensors)
+
+
+def log_softmax(logits: Sequence[Tensor]) -> list[Tensor]:
+    """Row log-softmax of ``B`` contiguous CUDA float32 ``(T_i, V_i)`` logits.
+
+    Per row, with ``m = max(x)`` and ``ls = log(sum(exp(x - m)))`` summed in
+    one fixed order, returns ``(x - m) - ls`` (torch's formula; within a few
+    ulp of ``torch.log_softmax``): exactly the values ``align_logits`` aligns.
+    Enqueued on the current stream; no host synchronization.
+    """
+    if not 0 < len(logits) <= 65535:
+        raise ValueError("provide 1..65535 logit tensors")
+    if not (isinstance(logits[0], Tensor) and logits[0].is_cuda):
+        raise ValueError("logits must be contiguous CUDA float32 [T,V] with supported dimensions on one device")
+    load_extension()
+    return _native.log_softmax(logits)
+
+
 @dataclass(frozen=True)
 class TokenSpans:
     """Token spans of an alignment: ``spans`` int64 ``(sum(lengths), 2)`` holds,

@@ -19,7 +19,8 @@ FFA_MAX_VOCAB = 8192
 FFA_MAX_STATES = 20479
 
 EXPORTED = ("ffa_default_options", "ffa_align_plan_batch", "ffa_align_describe", "ffa_align_launch",
-            "ffa_emission_validity_launch", "ffa_token_spans_launch", "ffa_last_error", "ffa_profile_next_launch")
+            "ffa_emission_validity_launch", "ffa_token_spans_launch", "ffa_log_softmax_launch", "ffa_last_error",
+            "ffa_profile_next_launch")
 
 
 class SpanRecord(ctypes.Structure):
@@ -38,7 +39,12 @@ class Options(ctypes.Structure):
         "repair_budget_frames", "repair_threads", "trace_min_frames", "repair_min_frames",
         "frontier_min_frames")] + [(name, ctypes.c_int32) for name in (
             "compact_alphabet", "parallel_traceback", "overlap_fallback", "frontier_reuse", "check_inputs",
-            "reserved")]
+            "logits")]
+
+
+class LogitsRecord(ctypes.Structure):
+    _fields_ = [("logits", ctypes.c_void_p), ("log_probs", ctypes.c_void_p), ("frames", ctypes.c_int64),
+                ("vocab", ctypes.c_int64)]
 
 
 class Plan(ctypes.Structure):
@@ -75,6 +81,8 @@ def load(path: Path | str = HIP_LIBRARY) -> ctypes.CDLL:
     lib.ffa_profile_next_launch.argtypes = [p, p]
     lib.ffa_token_spans_launch.restype = ctypes.c_int
     lib.ffa_token_spans_launch.argtypes = [p, ctypes.c_int64, p, p, p, p]
+    lib.ffa_log_softmax_launch.restype = ctypes.c_int
+    lib.ffa_log_softmax_launch.argtypes = [p, ctypes.c_int64, ctypes.c_int64, p]
     return lib
 
 

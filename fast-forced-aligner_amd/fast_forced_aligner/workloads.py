@@ -84,35 +84,42 @@ def ctc_frame_labels(rng: np.random.Generator, targets: np.ndarray, frames: int,
 
 
 def peaky(rng: np.random.Generator, targets: np.ndarray, frames: int, vocab: int, blank: int = 0,
-          boost: float = 8.0) -> np.ndarray:
+          boost: float = 8.0, raw: bool = False) -> np.ndarray:
     labels = ctc_frame_labels(rng, targets, frames, blank)
     logits = rng.standard_normal((frames, vocab), dtype=np.float32)
     logits[np.arange(frames), labels] += np.float32(boost)
-    return _log_softmax(logits)
+    return logits if raw else _log_softmax(logits)
 
 
-def c1() -> Batch:
+# Every generator takes raw=True to return the logits before the log-softmax
+# (the input of the fused logits path); the random draws are the same.
+def _finish(x: np.ndarray, raw: bool) -> np.ndarray:
+    return x.astype(np.float32, copy=False) if raw else _log_softmax(x)
+
+
+def c1(raw: bool = False) -> Batch:
     import torch
 
     generator = torch.Generator().manual_seed(SEEDS["c1"])
-    emissions = [torch.randn(t, 32, generator=generator).log_softmax(-1).numpy() for t in (500, 320)]
+    logits = [torch.randn(t, 32, generator=generator) for t in (500, 320)]
+    emissions = [x.numpy() if raw else x.log_softmax(-1).numpy() for x in logits]
     targets = [np.array([3, 7, 7, 12], dtype=np.int64), np.array([4, 9, 2], dtype=np.int64)]
     return Batch("c1", emissions, targets)
 
 
-def c2(batch: int = 64) -> Batch:
+def c2(batch: int = 64, raw: bool = False) -> Batch:
     rng = np.random.default_rng(SEEDS["c2"])
     emissions, targets = [], []
     for _ in range(batch):
         T = int(rng.integers(250, 1751))
         L = int(round(T / 3.3))
         y = rng.integers(1, 32, size=L).astype(np.int64)
-        emissions.append(peaky(rng, y, T, 32))
+        emissions.append(peaky(rng, y, T, 32, raw=raw))
         targets.append(y)
     return Batch("c2", emissions, targets)
 
 
-def c3(batch: int = 4, frames: int = 30000, tokens: int = 9000) -> Batch:
+def c3(batch: int = 4, frames: int = 30000, tokens: int = 9000, raw: bool = False) -> Batch:
     rng = np.random.default_rng(SEEDS["c3"])
     emissions, targets = [], []
     for _ in range(batch):
@@ -128,12 +135,12 @@ def c3(batch: int = 4, frames: int = 30000, tokens: int = 9000) -> Batch:
             boost[start:start + width] = 0.0
             spans += width
         logits[np.arange(frames), labels] += boost
-        emissions.append(_log_softmax(logits))
+        emissions.append(_finish(logits, raw))
         targets.append(y)
     return Batch("c3", emissions, targets)
 
 
-def c4(batch: int = 128) -> Batch:
+def c4(batch: int = 128, raw: bool = False) -> Batch:
     rng = np.random.default_rng(SEEDS["c4"])
     ids = np.arange(1, 1024)
     p = ids.astype(np.float64) ** -1.1
@@ -143,12 +150,12 @@ def c4(batch: int = 128) -> Batch:
         T = int(rng.integers(125, 501))
         L = int(round(T / 6))
         y = rng.choice(ids, size=L, p=p).astype(np.int64)
-        emissions.append(peaky(rng, y, T, 1024))
+        emissions.append(peaky(rng, y, T, 1024, raw=raw))
         targets.append(y)
     return Batch("c4", emissions, targets)
 
 
-def c5(batch: int = 1024) -> Batch:
+def c5(batch: int = 1024, raw: bool = False) -> Batch:
     rng = np.random.default_rng(SEEDS["c5"])
     emissions, targets = [], []
     kinds = []
@@ -167,11 +174,11 @@ def c5(batch: int = 1024) -> Batch:
         else:
             kind = "peaky"
         if kind == "flat":
-            e = _log_softmax(rng.normal(0.0, 0.01, size=(T, 32)).astype(np.float32))
+            e = _finish(rng.normal(0.0, 0.01, size=(T, 32)).astype(np.float32), raw)
         elif kind == "infeasible":
-            e = _log_softmax(rng.standard_normal((T, 32), dtype=np.float32))
+            e = _finish(rng.standard_normal((T, 32), dtype=np.float32), raw)
         else:
-            e = peaky(rng, y, T, 32)
+            e = peaky(rng, y, T, 32, raw=raw)
         emissions.append(e)
         targets.append(y)
         kinds.append(kind)

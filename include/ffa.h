@@ -70,7 +70,12 @@ typedef struct ffa_align_options {
   int32_t overlap_fallback;
   int32_t frontier_reuse;
   int32_t check_inputs;
-  int32_t reserved;
+  /* 0: emissions are log-probabilities (the reference's input). 1: emissions
+   * are raw fp32 logits and the path aligns their row log-softmax, computed
+   * inside the kernels exactly as ffa_log_softmax_launch materializes it (no
+   * counterpart in the reference, whose callers run log_softmax first:
+   * examples/transformers_ctc/align.py:55-56). */
+  int32_t logits;
 } ffa_align_options;
 
 /* Sizes the caller allocates before ffa_align_launch. */
@@ -145,6 +150,26 @@ typedef struct ffa_span_record {
 
 int ffa_token_spans_launch(const ffa_span_record* device_records, int64_t count, const int64_t* labels,
                            const int32_t* status, int64_t* spans, hipStream_t stream);
+
+/* Row log-softmax of raw logits (the producer step before alignment,
+ * examples/transformers_ctc/align.py:55-56: logits.float().log_softmax(-1);
+ * this entry has no native counterpart in the reference). Per row, with
+ * m = max(x) (+0.0 for a zero maximum) and ls = logf(sum of expf(x - m)):
+ * out = (x - m) - ls. The sum's order is fixed (lane l of a 64-lane wave adds
+ * the terms of columns l, l+64, ... in turn from +0.0; the 64 partial sums then
+ * combine as s[l] += s[l + o] for o = 32, 16, ..., 1), so the values equal,
+ * bit for bit, the ones ffa_align_launch uses when options->logits is set.
+ * device_records: [count] records in device memory; max_frames: the largest
+ * `frames` among them (sizes the grid). */
+typedef struct ffa_logits_record {
+  const float* logits;  /* device, contiguous [frames][vocab] fp32 */
+  float* log_probs;     /* device, contiguous [frames][vocab] fp32; may not overlap logits */
+  int64_t frames;       /* 1 .. INT32_MAX */
+  int64_t vocab;        /* 1 .. FFA_MAX_VOCAB */
+} ffa_logits_record;
+
+int ffa_log_softmax_launch(const ffa_logits_record* device_records, int64_t count, int64_t max_frames,
+                           hipStream_t stream);
 
 /* Message for the last failing call on this thread. */
 const char* ffa_last_error(void);

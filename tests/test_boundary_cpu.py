@@ -185,3 +185,34 @@ def test_raise_for_status_messages():
     assert text == "; ".join(parts)
     with pytest.raises(RuntimeError, match="unknown alignment status"):
         _batch([0, 99]).raise_for_status()
+
+
+def test_logits_option_plans_statistics(lib):
+    shapes = [(500, 32, 4, 0), (320, 32, 3, 0)]
+    for optimized in (True, False):
+        rc, plain, _ = _plan(lib, shapes, optimized=optimized)
+        assert rc == 0
+        rc, fused, _ = _plan(lib, shapes, optimized=optimized, logits=1)
+        assert rc == 0
+        # 8 bytes of row statistics per frame, 256-byte aligned; same table
+        assert fused.workspace_bytes == plain.workspace_bytes + (8 * 820 + 255) // 256 * 256
+        assert fused.table_bytes == plain.table_bytes
+    rc, _, _ = _plan(lib, shapes, logits=2)
+    assert rc == -1 and "logits must be 0 or 1" in lib.ffa_last_error().decode()
+
+
+def test_logits_entry_points_check_arguments_on_the_host(lib):
+    assert lib.ffa_log_softmax_launch(None, 1, 10, None) == -1
+    assert "null record" in lib.ffa_last_error().decode()
+    assert lib.ffa_log_softmax_launch(None, 0, 10, None) == -1
+    assert lib.ffa_log_softmax_launch(None, 1, 0, None) == -1
+    e = torch.zeros(12, 6)
+    t = torch.tensor([1])
+    with pytest.raises(ValueError, match="contiguous CUDA"):
+        ffa.align_logits([e], [t])
+    with pytest.raises(ValueError, match="mode must be"):
+        ffa.align_logits([e], [t], mode="fast")
+    with pytest.raises(ValueError, match="1..65535"):
+        ffa.log_softmax([])
+    with pytest.raises(ValueError, match="contiguous CUDA"):
+        ffa.log_softmax([e])
