@@ -69,18 +69,18 @@ static_assert(sizeof(Slot) == 32, "slot layout");
 
 // Per-chunk table entry of optimized mode, 16 bytes so that a whole batch's
 // table usually stays small enough for the runtime's in-queue copy. It holds
-// what the row loads need, so they are issued before the record descriptor
-// arrives:
-//   word bits 0-15 record, 16-24 frames in the chunk - 1, 25-27 V/4 - 1 and
-//   bit 31 the greedy fast path (V <= 32, V % 4 == 0, 16-byte aligned rows,
-//   at most 128 frames, greedy shortcuts on).
+// what the target loads need, so they are issued together with the record
+// descriptor's load instead of after it:
+//   lo bits 0-44 the targets' address / 8 (48-bit GPU addresses), 45-58 U,
+//      59 the greedy fast path (V <= 32, V % 4 == 0, 16-byte aligned rows, at
+//      most 128 frames, greedy shortcuts on), 60-62 V/4 - 1 (fast path)
+//   hi bits 0-15 record, 16-24 frames in the chunk - 1, 25-55 chunk index.
 struct ChunkEntry {
-  const float* rows;  // first emission row of the chunk
-  uint32_t word;
-  int32_t chunk;
+  uint64_t lo, hi;
 };
 static_assert(sizeof(ChunkEntry) == 16, "chunk entry layout");
-constexpr uint32_t CHUNK_FAST = 1u << 31;
+constexpr int ENTRY_U_SHIFT = 45, ENTRY_FAST_SHIFT = 59, ENTRY_QUADS_SHIFT = 60;
+
 
 struct Params {
   const RecordDesc* desc;
@@ -217,6 +217,7 @@ __device__ inline void store_pod(GLB T* dst, const T& value) {
 #pragma unroll
   for (size_t i = 0; i < sizeof(T) / 16; ++i) ((GLB v4i_t*)dst)[i] = tmp[i];
 }
+
 
 // ---------------------------------------------------------------------------
 // Wave64 helpers.
@@ -808,13 +809,7 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
 }
 
 // ---------------------------------------------------------------------------
-// Target staging and validation (pack_inputs, cu:819-877), done by every
-// workgroup that needs the record: copies the targets into LDS as int16,
-// computes the status and the transcript alphabet (cu:53-58). For V <= 32 the
-// alphabet is returned as a bit mask; otherwise it is left in L.bitmap.
-// Out-of-vocabulary ids are rejected (status 3) even unchecked: the reference
-// reads out of bounds there (py:400-402); this build never reads outside the
-// emission rows.
+// Result of target staging (stage_targets below).
 struct Staged {
   int status;
   uint32_t alpha32;
@@ -847,19 +842,47 @@ __device__ inline uint32_t tri_key(int x0, int x1, int x2, bool small) {
                : (((uint32_t)x0 * 40503u + (uint32_t)x1 * 30011u + (uint32_t)x2 * 52511u) & 0xffffu);
 }
 
-// Target staging and validation (pack_inputs, cu:819-877), done by every
-// workgroup that needs the record: copies the targets into LDS as int16,
-// computes the status and the transcript alphabet (cu:53-58). For V <= 32 the
-// alphabet is returned as a bit mask; otherwise it is left in L.bitmap. With
-// `keys`, the placement prefilter keys of every target position are built too.
-// Out-of-vocabulary ids are rejected (status 3) even unchecked: the reference
-// reads out of bounds there (py:400-402); this build never reads outside the
-// emission rows. One workgroup barrier.
-__device__ __attribute__((always_inline)) Staged stage_targets(const GLB int64_t* y, int U, int V, int blank, int64_t T, int rec,
-                                const Params& p, const Lds& L, int alphabet, bool keys) {
+// The first batch of a thread's targets, loaded before the values that the
+// checks need (V, blank, T) are known. Thread k owns targets
+// [k*per, (k+1)*per), per = ceil(U / threads), processed in batches of 8 with
+// the one before (repeat count) and the two after (keys). Every thread loads
+// with clamped indices and no branch, so the compiler can wait for these
+// loads without waiting for loads issued after them (the chunk's rows). An
+// empty transcript reads the descriptor table instead (values unused).
+struct TargetLoads {
+  const GLB int64_t* ys;
+  int U, j0, j1, jlast;
+  int64_t before;
+  int64_t v[10];
+};
+
+__device__ __attribute__((always_inline)) inline void load_target_batch(TargetLoads& t, int jb) {
+#pragma unroll
+  for (int q = 0; q < 10; ++q) t.v[q] = t.ys[min(jb + q, t.jlast)];
+}
+
+__device__ __attribute__((always_inline)) inline TargetLoads issue_targets(const GLB int64_t* y, int U, const Params& p) {
+  TargetLoads t;
+  const int per = (U + (int)blockDim.x - 1) / (int)blockDim.x;
+  t.U = U;
+  t.j0 = threadIdx.x * per;
+  t.j1 = min(U, t.j0 + per);
+  t.ys = U > 0 ? y : (const GLB int64_t*)glb(p.desc);
+  t.jlast = max(min(U, t.j1 + 2) - 1, 0);  // two past the range: the keys' lookahead
+  t.before = t.ys[min(max(t.j0 - 1, 0), max(U - 1, 0))];  // compared only for j > 0
+  load_target_batch(t, min(t.j0, t.jlast));
+  return t;
+}
+
+// Checks and LDS staging of the loaded targets (see stage_targets),
+// specialized for the alphabet form and the keys.
+template <int ALPHABET, bool KEYS>
+__device__ __attribute__((always_inline)) Staged finish_targets(TargetLoads& t, int V, int blank, int64_t T, int rec,
+                                                                 const Params& p, const Lds& L) {
   Header* h = L.h;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
-  if (alphabet == ALPHABET_BITMAP) {
+  const int U = t.U, j0 = t.j0, j1 = t.j1;
+  if constexpr (ALPHABET == ALPHABET_BITMAP) {
     for (int w = tid; w < (V + 31) / 32; w += blockDim.x) L.bitmap[w] = 0;
     __syncthreads();
     if (tid == 0) atomicOr(&L.bitmap[blank >> 5], 1u << (blank & 31));
@@ -867,29 +890,30 @@ __device__ __attribute__((always_inline)) Staged stage_targets(const GLB int64_t
   bool oov = false, bin = false;
   int repeats = 0;
   uint32_t mask = 0;
-  // thread t checks targets [t*per, (t+1)*per) and compares its first one with
-  // the target before it: one batch of loads in flight per thread
-  const int per = (U + (int)blockDim.x - 1) / (int)blockDim.x;
-  const int j0 = tid * per, j1 = min(U, j0 + per);
-  int64_t before = (j0 > 0 && j0 < U) ? y[j0 - 1] : 0;
+  int64_t before = t.before;
   for (int jb = j0; jb < j1; jb += 8) {
-    int64_t v[8];
+    if (jb > j0) load_target_batch(t, jb);
+    int tv[10];  // the staged int16 value of target jb+q: 0 when out of vocabulary, -1 past the end
 #pragma unroll
-    for (int q = 0; q < 8; ++q) v[q] = y[min(jb + q, j1 - 1)];
+    for (int q = 0; q < 10; ++q) {
+      const int64_t tok = t.v[q];
+      tv[q] = jb + q < U ? ((tok < 0 || tok >= V) ? 0 : (int)tok) : -1;
+    }
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       const int j = jb + q;
       if (j < j1) {
-        const int64_t tok = v[q];
+        const int64_t tok = t.v[q];
         const bool out = tok < 0 || tok >= V;  // checked as int64 before narrowing (cu:860)
         oov |= out;
         bin |= !out && tok == blank;
         repeats += j > 0 && tok == before;  // cu:861
         before = tok;
-        L.ytok[j] = (int16_t)(out ? 0 : tok);
+        L.ytok[j] = (int16_t)tv[q];
+        if constexpr (KEYS) L.key3[j] = (uint16_t)tri_key(tv[q], tv[q + 1], tv[q + 2], ALPHABET == ALPHABET_MASK32);
         if (!out) {
-          if (alphabet == ALPHABET_BITMAP) atomicOr(&L.bitmap[tok >> 5], 1u << (tok & 31));
-          else if (alphabet == ALPHABET_MASK32) mask |= 1u << tok;
+          if constexpr (ALPHABET == ALPHABET_BITMAP) atomicOr(&L.bitmap[tok >> 5], 1u << (tok & 31));
+          if constexpr (ALPHABET == ALPHABET_MASK32) mask |= 1u << (tok & 31);
         }
       }
     }
@@ -899,7 +923,7 @@ __device__ __attribute__((always_inline)) Staged stage_targets(const GLB int64_t
   // wave reductions: ballots for the flags, DPP scans for the count and the mask
   const int wf = (__ballot(oov) != 0 ? 1 : 0) | (__ballot(bin) != 0 ? 2 : 0);
   const int wr = __builtin_amdgcn_readlane(wave_scan_dpp(repeats), 63);
-  const int wm = __builtin_amdgcn_readlane(wave_or_scan_dpp((int)mask), 63);
+  const int wm = ALPHABET == ALPHABET_MASK32 ? __builtin_amdgcn_readlane(wave_or_scan_dpp((int)mask), 63) : 0;
   if (lane == 0) {
     h->stg_f[wave] = wf;
     h->stg_r[wave] = wr;
@@ -907,15 +931,11 @@ __device__ __attribute__((always_inline)) Staged stage_targets(const GLB int64_t
   }
   __syncthreads();
   int flags = 0, reps = 0;
-  uint32_t m = alphabet == ALPHABET_MASK32 ? 1u << blank : 0u;
+  uint32_t m = ALPHABET == ALPHABET_MASK32 ? 1u << blank : 0u;
   for (int w = 0; w < nw; ++w) {
     flags |= h->stg_f[w];
     reps += h->stg_r[w];
     m |= h->stg_m[w];
-  }
-  if (keys) {
-    const bool small = V <= 32;
-    for (int j = j0; j < j1; ++j) L.key3[j] = (uint16_t)tri_key(L.ytok[j], L.ytok[j + 1], L.ytok[j + 2], small);
   }
   Staged st;
   st.alpha32 = m;
@@ -927,8 +947,25 @@ __device__ __attribute__((always_inline)) Staged stage_targets(const GLB int64_t
   return st;
 }
 
-__device__ inline Staged stage_tokens(const RecordDesc& d, const Params& p, int rec, const Lds& L, int alphabet) {
-  return stage_targets(glb(d.targets), d.tokens, d.vocab, d.blank, d.frames, rec, p, L, alphabet, false);
+// Target staging and validation (pack_inputs, cu:819-877), done by every
+// workgroup that needs the record: copies the targets into LDS as int16,
+// computes the status and the transcript alphabet (cu:53-58). For V <= 32 the
+// alphabet is returned as a bit mask; otherwise it is left in L.bitmap. With
+// `keys`, the placement prefilter keys of every target position are built too
+// (from registers: each thread loads two targets past its range). Out-of-
+// vocabulary ids are rejected (status 3) even unchecked: the reference reads
+// out of bounds there (py:400-402); this build never reads outside the
+// emission rows. One workgroup barrier.
+template <int ALPHABET, bool KEYS>
+__device__ __attribute__((always_inline)) Staged stage_targets(const GLB int64_t* y, int U, int V, int blank, int64_t T,
+                                                                int rec, const Params& p, const Lds& L) {
+  TargetLoads t = issue_targets(y, U, p);
+  return finish_targets<ALPHABET, KEYS>(t, V, blank, T, rec, p, L);
+}
+
+template <int ALPHABET>
+__device__ inline Staged stage_tokens(const RecordDesc& d, const Params& p, int rec, const Lds& L) {
+  return stage_targets<ALPHABET, false>(glb(d.targets), d.tokens, d.vocab, d.blank, d.frames, rec, p, L);
 }
 
 __device__ inline bool legal_seam(const Rec& r, int start, int before) {  // cu:157-161
@@ -1184,17 +1221,32 @@ __device__ __attribute__((always_inline)) int greedy_chunk(const Rec& r, const L
 // Reads a descriptor every lane needs: 16-byte vector loads (one request per
 // instruction for the whole wave), then readfirstlane into scalar registers.
 template <class T>
-__device__ inline T load_uniform(const T* x) {
+struct Pending {  // a descriptor whose loads are issued but not yet waited for
+  v4i_t raw[sizeof(T) / 16];
+};
+
+template <class T>
+__device__ inline Pending<T> issue_uniform(const T* x) {
   static_assert(sizeof(T) % 16 == 0, "16-byte granules");
-  v4i_t tmp[sizeof(T) / 16];
+  Pending<T> out;
 #pragma unroll
-  for (size_t i = 0; i < sizeof(T) / 16; ++i) tmp[i] = ((const GLB v4i_t*)x)[i];
+  for (size_t i = 0; i < sizeof(T) / 16; ++i) out.raw[i] = ((const GLB v4i_t*)x)[i];
+  return out;
+}
+
+template <class T>
+__device__ inline T finish_uniform(const Pending<T>& x) {
   int w[sizeof(T) / 4];
 #pragma unroll
-  for (size_t i = 0; i < sizeof(T) / 4; ++i) w[i] = __builtin_amdgcn_readfirstlane(tmp[i / 4][i % 4]);
+  for (size_t i = 0; i < sizeof(T) / 4; ++i) w[i] = __builtin_amdgcn_readfirstlane(x.raw[i / 4][i % 4]);
   T out;
   __builtin_memcpy(&out, w, sizeof(T));
   return out;
+}
+
+template <class T>
+__device__ inline T load_uniform(const T* x) {
+  return finish_uniform(issue_uniform(x));
 }
 
 // Substring placement of a chunk's greedy path by wave 0 (blank-free
@@ -1353,7 +1405,40 @@ __device__ __attribute__((always_inline)) int place_wave(const Lds& L, int g0, i
 // unique iff exactly one column equals it. Wave 0 then places the chunk while
 // wave 1 computes the serial fp32 chunk objective (cu:135-137). Writes the
 // labels and scores of an accepted chunk; *g / *fs return the lane's frame.
-__device__ __attribute__((always_inline)) int greedy_fast(const Lds& L, const float (&x)[32], int n, int U, int S, int V, int blank,
+// Per-row maximum of a lane's row over the columns in `cols` (others -inf):
+// the value, the number of columns equal to it and the last such column.
+struct RowMax {
+  float mx;
+  int count, idx;
+};
+
+__device__ __attribute__((always_inline)) inline RowMax row_max(const float (&x)[32], uint32_t cols) {
+  float v[32];
+#pragma unroll
+  for (int c = 0; c < 32; ++c) v[c] = (cols >> c) & 1u ? x[c] : NEG_INF;
+  float t[16];
+#pragma unroll
+  for (int c = 0; c < 16; ++c) t[c] = fmaxf(v[2 * c], v[2 * c + 1]);
+#pragma unroll
+  for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+    for (int c = 0; c < w; ++c) t[c] = fmaxf(t[2 * c], t[2 * c + 1]);
+  RowMax r{t[0], 0, -1};
+#pragma unroll
+  for (int c = 0; c < 32; ++c) {
+    const bool e = v[c] == r.mx;
+    r.count += e;
+    r.idx = e ? c : r.idx;
+  }
+  return r;
+}
+
+// `whole`: row_max over all 32 register columns (columns past V hold -inf),
+// computed before the transcript alphabet is known. When its maximum is unique and its column is
+// in the alphabet, it is also the unique maximum over the alphabet (cu:53-58
+// scan); any other lane of the wave has the alphabet-restricted maximum
+// computed here.
+__device__ __attribute__((always_inline)) int greedy_fast(const Lds& L, const float (&x)[32], RowMax whole, int n, int U, int S, int V, int blank,
                            uint32_t alpha32, bool blank_in, bool at_start, bool at_end, Slot& out, int* ambiguous,
                            int* g_lane, float* fs_lane) {
   Header* h = L.h;
@@ -1361,31 +1446,11 @@ __device__ __attribute__((always_inline)) int greedy_fast(const Lds& L, const fl
   int g = -2;
   float fs = -0.0f;  // identity of the fp32 sum for padding frames
   if (tid < 128) {
-    const uint32_t cols = V >= 32 ? 0xffffffffu : ((1u << V) - 1u);
-    float v[32];
-    if ((alpha32 & cols) == cols) {
-#pragma unroll
-      for (int c = 0; c < 32; ++c) v[c] = x[c];
-    } else {
-#pragma unroll
-      for (int c = 0; c < 32; ++c) v[c] = (alpha32 >> c) & 1u ? x[c] : NEG_INF;
-    }
-    float t[16];
-#pragma unroll
-    for (int c = 0; c < 16; ++c) t[c] = fmaxf(v[2 * c], v[2 * c + 1]);
-#pragma unroll
-    for (int w = 8; w >= 1; w >>= 1)
-#pragma unroll
-      for (int c = 0; c < w; ++c) t[c] = fmaxf(t[2 * c], t[2 * c + 1]);
-    const float mx = t[0];
-    int count = 0, idx = -1;
-#pragma unroll
-    for (int c = 0; c < 32; ++c) {
-      const bool e = v[c] == mx;
-      count += e;
-      idx = e ? c : idx;
-    }
     const bool live = tid < n;
+    const bool redo = live && !(whole.count == 1 && ((alpha32 >> whole.idx) & 1u));
+    if (__ballot(redo) != 0) whole = row_max(x, alpha32);
+    const float mx = whole.mx;
+    const int count = whole.count, idx = whole.idx;
     const bool bad = live && (!isfinite(mx) || count != 1);
     if (live) { g = idx; fs = mx; }
     L.g[tid] = g;
@@ -1437,7 +1502,7 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) conventional_kernel(Param
   const RecordDesc d = load_pod(glb(p.desc) + rec);
   Rec r = make_rec(d, p, L);
   if (LG) r.st = p.stats + d.frame_offset;
-  const Staged st = stage_tokens(d, p, rec, L, ALPHABET_NONE);
+  const Staged st = stage_tokens<ALPHABET_NONE>(d, p, rec, L);
   if (threadIdx.x == 0) {
     glb(p.stitched)[rec] = 0;
     glb(p.repair_passes)[rec] = 0;
@@ -1718,19 +1783,27 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
   const int slot_index = xcd_slot(blockIdx.x, p.total_slots);
   if (slot_index >= p.total_slots) return;
   const ChunkEntry ce = load_uniform(p.chunks + slot_index);
-  const int rec = (int)(ce.word & 0xffffu);
-  const int n = (int)((ce.word >> 16) & 0x1ffu) + 1;
-  const bool fast = (ce.word & CHUNK_FAST) != 0;
-  const int64_t a = (int64_t)ce.chunk * p.H;
+  const int rec = (int)(ce.hi & 0xffffu);
+  const int n = (int)((ce.hi >> 16) & 0x1ffu) + 1;
+  const int64_t chunk = (int64_t)(ce.hi >> 25);
+  const bool fast = ((ce.lo >> ENTRY_FAST_SHIFT) & 1u) != 0;
+  const int quads = (int)((ce.lo >> ENTRY_QUADS_SHIFT) & 7u) + 1;  // V / 4 (fast path)
+  const int U = (int)((ce.lo >> ENTRY_U_SHIFT) & 0x3fffu);
+  const GLB int64_t* y = (const GLB int64_t*)((ce.lo & ((1ull << ENTRY_U_SHIFT) - 1)) << 3);
+  const int64_t a = chunk * p.H;
   const int64_t b = a + n;
-  // The chunk's rows first, so their latency overlaps the record descriptor
-  // and target staging: lane f of waves 0-1 loads row a+f (fast path only).
+  // The record descriptor and the first batch of targets are requested
+  // together (the entry holds the targets' address and count); the chunk's
+  // rows follow as soon as the descriptor is in (fast path: lane f of waves
+  // 0-1 loads row a+f).
+  const Pending<RecordDesc> pd = issue_uniform(p.desc + rec);
+  TargetLoads tl = issue_targets(y, U, p);
+  const RecordDesc d = finish_uniform(pd);
   float x[32];
 #pragma unroll
   for (int q = 0; q < 32; ++q) x[q] = NEG_INF;
-  const int quads = (int)((ce.word >> 25) & 7u) + 1;  // V / 4 (fast path)
   if (fast && tid < n) {
-    const GLB v4f_t* src = (const GLB v4f_t*)glb(ce.rows) + (int64_t)tid * quads;
+    const GLB v4f_t* src = (const GLB v4f_t*)glb(d.emissions + a * (int64_t)d.vocab) + (int64_t)tid * quads;
 #pragma unroll
     for (int q = 0; q < 8; ++q)
       if (q < quads) {
@@ -1738,19 +1811,23 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
         x[4 * q] = v.x; x[4 * q + 1] = v.y; x[4 * q + 2] = v.z; x[4 * q + 3] = v.w;
       }
   }
-  const RecordDesc d = load_uniform(p.desc + rec);
-  // logits, fast path: each lane normalizes its own row in registers while the
-  // descriptor is in flight
+  const Staged st = fast ? finish_targets<ALPHABET_MASK32, true>(tl, d.vocab, d.blank, d.frames, rec, p, L)
+                   : p.mode == 2 ? finish_targets<ALPHABET_BITMAP, false>(tl, d.vocab, d.blank, d.frames, rec, p, L)
+                                 : finish_targets<ALPHABET_NONE, false>(tl, d.vocab, d.blank, d.frames, rec, p, L);
   float2 row_st = make_float2(0.0f, 0.0f);
-  if (LG && fast && tid < n) {
-    row_st = lane_row_stats(x, 4 * quads);
+  RowMax whole{NEG_INF, 0, -1};
+  if (fast && tid < 128) {
+    if (LG && tid < n) {  // logits: each lane normalizes its own row in registers
+      row_st = lane_row_stats(x, 4 * quads);
 #pragma unroll
-    for (int c = 0; c < 32; ++c)
-      if (c < 4 * quads) x[c] = lsm(x[c], row_st);
-    L.st[tid] = row_st;
+      for (int c = 0; c < 32; ++c)
+        if (c < 4 * quads) x[c] = lsm(x[c], row_st);
+      L.st[tid] = row_st;
+    }
+    if (p.mode == 2) whole = row_max(x, 0xffffffffu);
   }
-  const Staged st = stage_targets(glb(d.targets), d.tokens, d.vocab, d.blank, d.frames, rec, p, L,
-                                  p.mode != 2 ? ALPHABET_NONE : (fast ? ALPHABET_MASK32 : ALPHABET_BITMAP), fast);
+  // (L.st is complete before any DP of this chunk reads it: greedy_fast's
+  // barrier comes first)
   if (LG) {  // the tail kernel's DP reads the statistics from global memory
     if (fast) {
       if (tid < n) store_stats(glb(p.stats) + d.frame_offset + a + tid, row_st);
@@ -1775,7 +1852,7 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
     if (p.mode == 2 && fast) {
       int g;
       float fs;
-      accepted = greedy_fast(L, x, n, d.tokens, 2 * d.tokens + 1, d.vocab, d.blank, st.alpha32, st.blank_in,
+      accepted = greedy_fast(L, x, whole, n, d.tokens, 2 * d.tokens + 1, d.vocab, d.blank, st.alpha32, st.blank_in,
                              a == 0, b == d.frames, out, &ambiguous, &g, &fs);
       if (accepted && tid < n) {  // finish's label/score gather collapses to g and fs (cu:642-667)
         labels[tid] = g;
@@ -1787,7 +1864,7 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
       if (LG) { r.st = L.st; r.st_first = a; }
       if (p.mode == 2 && !fast) accepted = greedy_chunk(r, L, a, b, st.blank_in, out, &ambiguous);
       if (!accepted) {  // initial chunk DP (cu:721-726), relaxed init for a > 0
-        GLB float* fr = r.frontier ? r.frontier + (int64_t)ce.chunk * r.S : nullptr;
+        GLB float* fr = r.frontier ? r.frontier + chunk * r.S : nullptr;
         const DPOut o = dp_interval<K, D, LG>(r, L, a, b, b == r.T, nullptr, a + 1, fr, TRACE_ALWAYS);
         out.objective = o.score;
         out.end = o.terminal;
@@ -2153,6 +2230,8 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
       return fail(FFA_E_INVALID, "resident input shape or blank outside supported range");
     if (!r.emissions || (r.tokens > 0 && !r.targets))
       return fail(FFA_E_INVALID, "null emission or target pointer");
+    if ((reinterpret_cast<uintptr_t>(r.targets) & 7) != 0 || (reinterpret_cast<uintptr_t>(r.targets) >> 48) != 0)
+      return fail(FFA_E_INVALID, "target pointer not 8-byte aligned inside the 48-bit GPU address space");
     const int S = states_of(r);
     total_frames += r.frames;
     bp_words += r.frames * stride_of(S);
@@ -2266,12 +2345,14 @@ int ffa_align_describe(const ffa_align_plan* plan, const ffa_record* records, vo
       // one frame per lane of two waves
       const bool fast = in[I_MODE] == 2 && H <= 128 && r.vocab <= 32 && r.vocab % 4 == 0 &&
                         (reinterpret_cast<uintptr_t>(r.emissions) & 15) == 0;
-      const uint32_t tag = fast ? (ffa::CHUNK_FAST | (uint32_t)(r.vocab / 4 - 1) << 25) : 0u;
+      const uint64_t lo = (uint64_t)reinterpret_cast<uintptr_t>(r.targets) >> 3 |
+                          (uint64_t)r.tokens << ffa::ENTRY_U_SHIFT |
+                          (fast ? (1ull << ffa::ENTRY_FAST_SHIFT | (uint64_t)(r.vocab / 4 - 1) << ffa::ENTRY_QUADS_SHIFT)
+                                : 0ull);
       for (int64_t c = 0; c < n; ++c) {
         ffa::ChunkEntry& e = chunks[slot + c];
-        e.rows = r.emissions + c * H * r.vocab;
-        e.word = (uint32_t)i | (uint32_t)(std::min<int64_t>(H, r.frames - c * H) - 1) << 16 | tag;
-        e.chunk = (int32_t)c;
+        e.lo = lo;
+        e.hi = (uint64_t)i | (uint64_t)(std::min<int64_t>(H, r.frames - c * H) - 1) << 16 | (uint64_t)c << 25;
       }
       slot += (int32_t)n;
     }
