@@ -181,6 +181,83 @@ def cpu_baseline(batch, seconds=10.0):
                       f"one record per thread"}
 
 
+def matrix(path: str) -> int:
+    """Every config of BASELINE.json in both modes, with and without
+    check_inputs, by the reference's timing contract (benchmarks/README.md:
+    165-200 as restated for this path): inputs resident; single-call latency
+    (host sync, one align, host sync) and pipelined time per call (K calls back
+    to back, no sync in between), each the median of repeats; the dominant
+    kernel's duration from HIP events; parity of labels, scores, status and
+    objective with the CPU oracle, bit for bit; the oracle's conventional DP on
+    the host cores as the CPU baseline. Writes a markdown table to `path` and
+    prints one JSON line per row."""
+    import statistics
+
+    import numpy as np
+    import torch
+
+    import fast_forced_aligner as ffa
+    from fast_forced_aligner import capi, workloads
+    from oracle import oracle
+
+    ffa.load_extension()
+    capi_lib = capi.load()
+    hip = hip_runtime()
+    rows = []
+    header = ("| Config | Mode | check_inputs | Single call (ms) | Pipelined (ms/call) | Aligned frames/s | "
+              "DP cells/s | Dominant kernel (µs) | % HBM roofline | Parity vs oracle | CPU baseline frames/s |")
+    for name in ("c1", "c2", "c3", "c4", "c5"):
+        batch = workloads.make(name)
+        es = [torch.from_numpy(e).to("cuda:0") for e in batch.emissions]
+        ys = [torch.from_numpy(y).to("cuda:0") for y in batch.targets]
+        cpu = cpu_baseline(batch, seconds=3.0)
+        for mode in ("conventional", "optimized"):
+            for check in (True, False):
+                def call():
+                    return ffa.align(es, ys, mode=mode, check_inputs=check)
+
+                result = call()
+                torch.cuda.synchronize()
+                singles = []
+                for _ in range(7):
+                    t0 = time.perf_counter()
+                    call()
+                    torch.cuda.synchronize()
+                    singles.append(time.perf_counter() - t0)
+                single = statistics.median(singles)
+                k = max(3, min(100, int(0.3 / single)))
+                piped, kernels = [], []
+                for _ in range(5):
+                    step_s, kernel_ms, result = measure(capi_lib, hip, call, k, 2)
+                    piped.append(step_s)
+                    kernels.append(kernel_ms)
+                step = statistics.median(piped)
+                kernel_ms = statistics.median(kernels)
+                want = oracle.align(batch.emissions, batch.targets, mode=mode, check_inputs=check, threads=16)
+                got = {f: getattr(result, f).cpu().numpy() for f in ("labels", "scores", "status", "objective")}
+                parity = all(np.array_equal(got[f].view(np.int32) if got[f].dtype == np.float32 else got[f],
+                                            want[f].view(np.int32) if want[f].dtype == np.float32 else want[f])
+                             for f in got)
+                frac = batch.min_bytes() / (kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS
+                row = {"config": name, "mode": mode, "check_inputs": check, "single_call_ms": single * 1e3,
+                       "pipelined_ms": step * 1e3, "calls_per_repeat": k, "frames_per_s": batch.frames / step,
+                       "dp_cells_per_s": batch.cells / step, "kernel_us": kernel_ms * 1e3,
+                       "roofline_frac": frac, "parity_vs_oracle": parity, "cpu_frames_per_s": cpu["value"],
+                       "cpu_cores": cpu["cores"], "records": len(es), "frames": batch.frames,
+                       "algorithmic_bytes": batch.min_bytes()}
+                print(json.dumps(row), flush=True)
+                rows.append(row)
+    lines = [header, "|" + "---|" * 11]
+    for r in rows:
+        lines.append(f"| {r['config'].upper()} ({r['records']} records, {r['frames']} frames) | {r['mode']} | "
+                     f"{r['check_inputs']} | {r['single_call_ms']:.3f} | {r['pipelined_ms']:.3f} | "
+                     f"{r['frames_per_s']:.3g} | {r['dp_cells_per_s']:.3g} | {r['kernel_us']:.1f} | "
+                     f"{100 * r['roofline_frac']:.2f} | {'bit-exact' if r['parity_vs_oracle'] else 'MISMATCH'} | "
+                     f"{r['cpu_frames_per_s']:.3g} ({r['cpu_cores']} threads) |")
+    Path(path).write_text("\n".join(lines) + "\n")
+    return 0 if all(r["parity_vs_oracle"] for r in rows) else 1
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -190,6 +267,9 @@ def main() -> int:
     parser.add_argument("--mode", default="optimized", choices=["optimized", "conventional"])
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     parser.add_argument("--no-conventional", action="store_true", help="skip the conventional-mode figures")
+    parser.add_argument("--matrix", metavar="PATH",
+                        help="instead of the bench line: measure every config in both modes (single-call and "
+                             "pipelined times, kernel, roofline, parity, CPU baseline) and write a markdown table")
     parser.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                         help="after the timed work, run 10 plain device copies of MIB MiB (a known-size "
                              "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE counter passes)")
@@ -199,6 +279,8 @@ def main() -> int:
               f"(records are independent; see DESIGN.md for how a batch would shard). Got --gpus {args.gpus}.",
               file=sys.stderr)
         return 2
+    if args.matrix:
+        return matrix(args.matrix)
 
     import numpy as np
     import torch
