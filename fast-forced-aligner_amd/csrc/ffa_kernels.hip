@@ -640,9 +640,13 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
       float best = stay;
       Bits j = 0;
       if (adv > best) { best = adv; j = 1; }
-      bool take;
-      if constexpr (kMask) take = ((skm >> k) & 1u) && skp > best;
-      else take = skp + skb[k] > best;
+      // s0 = tid*K is even, so state s0+k is a blank state for even k and the
+      // skip into it is never legal (cu:407): no comparison to make
+      bool take = false;
+      if ((k & 1) != 0) {
+        if constexpr (kMask) take = ((skm >> k) & 1u) && skp > best;
+        else take = skp + skb[k] > best;
+      }
       if (take) { best = skp; j = 2; }
       al[k] = best + evk[k];
       bits |= j << (2 * k);
