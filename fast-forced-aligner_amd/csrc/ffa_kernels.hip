@@ -571,6 +571,13 @@ __device__ inline int trace_path(const Rec& r, int64_t a, int64_t b, int termina
   return s;
 }
 
+// How the frame loop knows whether the workgroup has several waves: fixed
+// at compile time (single / multi) or read at run time.
+template <int MODE>
+struct Waves {
+  static constexpr int mode = MODE;  // 0 one wave, 1 several, 2 decided at run time
+};
+
 // LG: logits input (emission reads pass through lsm with r.st); a template
 // parameter so that the log-probability build carries none of it.
 template <int K, int D, bool LG>
@@ -622,11 +629,16 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
     __syncthreads();
   }
   // One frame of the recurrence (cu:438-444); strict '>' keeps stay > advance >
-  // skip on ties. `evk` holds e[t][l[s]] for this thread's states.
-  auto frame = [&](int64_t t, const float (&evk)[K]) {
+  // skip on ties. `evk` holds e[t][l[s]] for this thread's states. `waves`
+  // (a Waves<> tag) says whether the workgroup has more than one wave; for
+  // K = 4 the frame loops are compiled once for each case, so a single-wave
+  // workgroup carries no cross-wave exchange code.
+  auto frame = [&](auto waves, int64_t t, const float (&evk)[K]) {
+    constexpr int WM = decltype(waves)::mode;
+    const bool M = WM == 2 ? nwaves > 1 : WM == 1;
     float up1 = wave_shr1(al[K - 1], NEG_INF);
     float up2 = wave_shr1(al[K - 2], NEG_INF);
-    if (nwaves > 1 && lane == 0 && wave > 0) {
+    if (M && lane == 0 && wave > 0) {
       const int par = (int)((t - 1) & 1);
       up2 = h->xchg[par][wave - 1][0];
       up1 = h->xchg[par][wave - 1][1];
@@ -652,7 +664,7 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
       bits |= j << (2 * k);
     }
     if (active) store_row<K>(bp + t * (int64_t)r.stride, tid, bits);
-    if (nwaves > 1) {
+    if (M) {
       if (lane == 63) {
         h->xchg[t & 1][wave][0] = al[K - 2];
         h->xchg[t & 1][wave][1] = al[K - 1];
@@ -708,12 +720,23 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
       if (nb <= last) load_block(nb);
       const float* rows = L.eblk + half * F * EBLK_COLS;
       const int nf = (int)min((int64_t)F, last - tb + 1);
-      for (int f = 0; f < nf; ++f) {
-        float evk[K];
-        const float* row = rows + f * (int)V;
+      auto frames = [&](auto waves) {
+        for (int f = 0; f < nf; ++f) {
+          float evk[K];
+          const float* row = rows + f * (int)V;
 #pragma unroll
-        for (int k = 0; k < K; ++k) evk[k] = *(const float*)((const char*)row + lab[k]);
-        frame(tb + f, evk);
+          for (int k = 0; k < K; ++k) evk[k] = *(const float*)((const char*)row + lab[k]);
+          frame(waves, tb + f, evk);
+        }
+      };
+      // (K >= 8 only comes with more than 128 threads: always several waves)
+      if constexpr (K == 4) {
+        if (nwaves > 1) frames(Waves<1>{});
+        else frames(Waves<0>{});
+      } else if constexpr (K == 32) {
+        frames(Waves<2>{});
+      } else {
+        frames(Waves<1>{});
       }
       if (nb <= last) store_block(nb, L.eblk + (half ^ 1) * F * EBLK_COLS);
       __syncthreads();  // the next block is in LDS; this block's reads are done
@@ -741,26 +764,36 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
       for (int k = 0; k < K; ++k) evk[k] = lsm(evk[k], st);
     }
   };
-  int64_t t0 = start_t;
-  for (; t0 + D <= b; t0 += D) {
+  auto ring = [&](auto waves) {
+    int64_t t0 = start_t;
+    for (; t0 + D <= b; t0 += D) {
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-      apply(ev[d], es[d]);
-      frame(t0 + d, ev[d]);
-      const int64_t t = min(t0 + d + D, last);
-      const GLB float* row = e + t * V;
+      for (int d = 0; d < D; ++d) {
+        apply(ev[d], es[d]);
+        frame(waves, t0 + d, ev[d]);
+        const int64_t t = min(t0 + d + D, last);
+        const GLB float* row = e + t * V;
 #pragma unroll
-      for (int k = 0; k < K; ++k) ev[d][k] = ldg_at(row, lab[k]);
-      if (LG) es[d] = r.st[t - r.st_first];
+        for (int k = 0; k < K; ++k) ev[d][k] = ldg_at(row, lab[k]);
+        if (LG) es[d] = r.st[t - r.st_first];
+      }
     }
+    // remaining < D frames: their gathers are already in ev[0 .. b-t0-1]
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      if (t0 + d < b) {
+        apply(ev[d], es[d]);
+        frame(waves, t0 + d, ev[d]);
+      }
+  };
+  if constexpr (K == 4) {
+    if (nwaves > 1) ring(Waves<1>{});
+    else ring(Waves<0>{});
+  } else if constexpr (K == 32) {
+    ring(Waves<2>{});
+  } else {
+    ring(Waves<1>{});
   }
-  // remaining < D frames: their gathers are already in ev[0 .. b-t0-1]
-#pragma unroll
-  for (int d = 0; d < D; ++d)
-    if (t0 + d < b) {
-      apply(ev[d], es[d]);
-      frame(t0 + d, ev[d]);
-    }
   }
   if (save_frontier) {  // cu:451-454
 #pragma unroll
