@@ -636,11 +636,16 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
   auto frame = [&](auto waves, int64_t t, const float (&evk)[K]) {
     constexpr int WM = decltype(waves)::mode;
     const bool M = WM == 2 ? nwaves > 1 : WM == 1;
+    // The skip into a thread's first state s0 (even, a blank state) is never
+    // legal, so only the previous thread's last state is needed; the
+    // multi-wave loops for K <= 16 exchange just that value across waves (the
+    // other loops keep both, which measured faster for them).
+    constexpr bool kOneUp = K <= 16 && WM == 1;
     float up1 = wave_shr1(al[K - 1], NEG_INF);
-    float up2 = wave_shr1(al[K - 2], NEG_INF);
+    float up2 = kOneUp ? up1 : wave_shr1(al[K - 2], NEG_INF);
     if (M && lane == 0 && wave > 0) {
       const int par = (int)((t - 1) & 1);
-      up2 = h->xchg[par][wave - 1][0];
+      if constexpr (!kOneUp) up2 = h->xchg[par][wave - 1][0];
       up1 = h->xchg[par][wave - 1][1];
     }
     Bits bits = 0;
@@ -666,7 +671,7 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
     if (active) store_row<K>(bp + t * (int64_t)r.stride, tid, bits);
     if (M) {
       if (lane == 63) {
-        h->xchg[t & 1][wave][0] = al[K - 2];
+        if constexpr (!kOneUp) h->xchg[t & 1][wave][0] = al[K - 2];
         h->xchg[t & 1][wave][1] = al[K - 1];
       }
       __syncthreads();
@@ -721,13 +726,14 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
       const float* rows = L.eblk + half * F * EBLK_COLS;
       const int nf = (int)min((int64_t)F, last - tb + 1);
       auto frames = [&](auto waves) {
-        for (int f = 0; f < nf; ++f) {
+        auto one = [&](int f) {
           float evk[K];
           const float* row = rows + f * (int)V;
 #pragma unroll
           for (int k = 0; k < K; ++k) evk[k] = *(const float*)((const char*)row + lab[k]);
           frame(waves, tb + f, evk);
-        }
+        };
+        for (int f = 0; f < nf; ++f) one(f);
       };
       // (K >= 8 only comes with more than 128 threads: always several waves)
       if constexpr (K == 4) {
