@@ -267,6 +267,8 @@ def main() -> int:
     parser.add_argument("--mode", default="optimized", choices=["optimized", "conventional"])
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     parser.add_argument("--no-conventional", action="store_true", help="skip the conventional-mode figures")
+    parser.add_argument("--no-extras", action="store_true",
+                        help="skip the neighbouring entry points (emission scan, token spans, logits path)")
     parser.add_argument("--matrix", metavar="PATH",
                         help="instead of the bench line: measure every config in both modes (single-call and "
                              "pipelined times, kernel, roofline, parity, CPU baseline) and write a markdown table")
@@ -338,8 +340,9 @@ def main() -> int:
         line["conventional"] = {"ms_per_step": c_step * 1e3, "frames_per_s": batch.frames / c_step,
                                 "dp_cells_per_s": batch.cells / c_step, "kernel_us": c_kernel_ms * 1e3,
                                 "roofline_frac": c_achieved / HBM_PEAK_GBS}
-    line["extras"] = extras(ffa, es, ys, result)
-    line["extras"]["align_logits"] = logits_figures(ffa, capi_lib, hip, args.config, args.mode)
+    if not args.no_extras:
+        line["extras"] = extras(ffa, es, ys, result)
+        line["extras"]["align_logits"] = logits_figures(ffa, capi_lib, hip, args.config, args.mode)
     line["cpu_baseline"] = None if args.no_cpu else cpu_baseline(batch)
     if args.calibrate_copy > 0:
         src = torch.ones(args.calibrate_copy << 18, dtype=torch.float32, device=dev)

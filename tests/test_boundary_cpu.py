@@ -115,6 +115,31 @@ def test_plan_rejects_like_the_reference(lib, shape, changes, message):
     assert message in lib.ffa_last_error().decode()
 
 
+@pytest.mark.parametrize("address", [0x9004, 1 << 48])
+def test_plan_rejects_target_addresses_the_chunk_entries_cannot_hold(lib, address):
+    """Chunk entries carry the targets' address / 8 in 45 bits: the plan
+    rejects a pointer that is not 8-byte aligned or not below 2^48."""
+    o = capi.default_options(lib, True)
+    plan = capi.Plan()
+    recs = (capi.Record * 1)(capi.Record(0x1000, address, 50, 8, 2, 0))
+    assert lib.ffa_align_plan_batch(recs, 1, ctypes.byref(o), ctypes.byref(plan)) == -1
+    assert "48-bit" in lib.ffa_last_error().decode()
+
+
+def test_chunk_entries_hold_targets_address_and_counts(lib):
+    rc, plan, recs = _plan(lib, [(300, 32, 5, 0)])
+    assert rc == 0
+    buf = (ctypes.c_uint8 * plan.table_bytes)()
+    assert lib.ffa_align_describe(ctypes.byref(plan), recs, buf, plan.table_bytes) == 0
+    entries = (ctypes.c_uint64 * 6).from_buffer(buf, 64)  # after the one 64-byte record descriptor
+    for c in range(3):  # 300 frames: chunks of 128, 128, 44
+        lo, hi = entries[2 * c], entries[2 * c + 1]
+        assert (lo & ((1 << 45) - 1)) << 3 == recs[0].targets
+        assert (lo >> 45) & 0x3FFF == 5  # U
+        assert (lo >> 59) & 1 == 1 and ((lo >> 60) & 7) + 1 == 8  # fast path, V/4
+        assert hi & 0xFFFF == 0 and ((hi >> 16) & 0x1FF) + 1 == (128, 128, 44)[c] and hi >> 25 == c
+
+
 def test_operator_schemas_match_the_reference():
     torch.ops.load_library(str(alignment.TORCH_LIBRARY))
     for name, schema in REFERENCE_SCHEMAS.items():
