@@ -110,6 +110,15 @@ struct Params {
 // ---------------------------------------------------------------------------
 // Shared-memory layout. A fixed header followed by dynamic regions whose sizes
 // come from the launch (all offsets are uniform).
+// Per-record diagnostics of the tail kernel, kept in LDS by thread 0 so that
+// they hold no registers across the tail's DP calls.
+struct TailStats {
+  int64_t sc_accepted, sc_frames, sc_ambiguous;  // shortcut_stats
+  int64_t reuse[4];                              // reuse_stats
+  int64_t repaired;                              // repaired_frames
+  int early, rejected, maxprop, passes;          // routing_stats, repair_passes
+};
+
 struct Header {
   float xchg[2][16][2];  // DP neighbour values crossing wave boundaries
   float red_v[16];
@@ -124,6 +133,7 @@ struct Header {
   uint32_t stg_m[16];  // per-wave alphabet masks (V <= 32)
   int gbad[2];         // per-wave greedy rejection (fast path)
   int last;            // the record's outputs are written (tail fast path)
+  TailStats ts;
 };
 
 struct Lds {
@@ -735,12 +745,19 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
         };
         for (int f = 0; f < nf; ++f) one(f);
       };
-      // (K >= 8 only comes with more than 128 threads: always several waves)
+      // (K >= 8 only comes with more than 128 threads: always several waves;
+      // K = 32 keeps a plain loop, which spills less in the chunk and tail kernels)
       if constexpr (K == 4) {
         if (nwaves > 1) frames(Waves<1>{});
         else frames(Waves<0>{});
       } else if constexpr (K == 32) {
-        frames(Waves<2>{});
+        for (int f = 0; f < nf; ++f) {
+          float evk[K];
+          const float* row = rows + f * (int)V;
+#pragma unroll
+          for (int k = 0; k < K; ++k) evk[k] = *(const float*)((const char*)row + lab[k]);
+          frame(Waves<2>{}, tb + f, evk);
+        }
       } else {
         frames(Waves<1>{});
       }
@@ -795,8 +812,26 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
   if constexpr (K == 4) {
     if (nwaves > 1) ring(Waves<1>{});
     else ring(Waves<0>{});
-  } else if constexpr (K == 32) {
-    ring(Waves<2>{});
+  } else if constexpr (K == 32) {  // plain loop (spills less in the chunk and tail kernels)
+    int64_t t0 = start_t;
+    for (; t0 + D <= b; t0 += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        apply(ev[d], es[d]);
+        frame(Waves<2>{}, t0 + d, ev[d]);
+        const int64_t t = min(t0 + d + D, last);
+        const GLB float* row = e + t * V;
+#pragma unroll
+        for (int k = 0; k < K; ++k) ev[d][k] = ldg_at(row, lab[k]);
+        if (LG) es[d] = r.st[t - r.st_first];
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      if (t0 + d < b) {
+        apply(ev[d], es[d]);
+        frame(Waves<2>{}, t0 + d, ev[d]);
+      }
   } else {
     ring(Waves<1>{});
   }
@@ -1649,24 +1684,24 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
     if (h->ibuf[6]) return;
     __syncthreads();
   }
-  int64_t sc_accepted = 0, sc_frames = 0, sc_ambiguous = 0;
-  int64_t reuse0 = 0, reuse1 = 0, reuse2 = 0, reuse3 = 0;
+  TailStats& ts = h->ts;  // written by thread 0 only
   if (tid == 0) {  // shortcut_stats (cu:129-133, 140-146) and frontier writes of the chunk DPs
+    ts = TailStats{};
     for (int k = 0; k < n; ++k) {
-      if (sl[k].kind == 1) { ++sc_accepted; sc_frames += sl[k].b - sl[k].a; }
+      if (sl[k].kind == 1) { ++ts.sc_accepted; ts.sc_frames += sl[k].b - sl[k].a; }
       else {
-        if (sl[k].kind == 2) ++sc_ambiguous;
-        if (frontier_on) reuse2 += S;
+        if (sl[k].kind == 2) ++ts.sc_ambiguous;
+        if (frontier_on) ts.reuse[2] += S;
       }
     }
   }
-  int early = 0, rejected = 0, maxprop = 0, passes = 0;
-  int64_t repaired = 0;
+  int early = 0;  // uniform copy of ts.early
   int status = 0;
   float objective = NEG_INF;
   const bool repairs = p.repair_rounds > 0;
   for (int round = 0; round < p.repair_rounds; ++round) {
     if (tid == 0) {  // plan_repairs, cu:164-228
+      early = ts.early;
       int run = !(p.overlap && early == 2);
       if (run && p.budget > 0 && T >= p.repair_min) {
         int before = -1;
@@ -1685,8 +1720,8 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
           before = k;
         }
         if (reject) {
-          ++rejected;
-          maxprop = max(maxprop, (int)maximum);
+          ++ts.rejected;
+          ts.maxprop = max(ts.maxprop, (int)maximum);
           if (p.overlap) early = 1;
           run = 0;
         }
@@ -1709,11 +1744,12 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
           previous = k;
         }
         if (merged) {
-          ++passes;
+          ++ts.passes;
           for (int k = 0; k < n; ++k)
-            if (sl[k].flag) repaired += sl[k].b - sl[k].a;
+            if (sl[k].flag) ts.repaired += sl[k].b - sl[k].a;
         }
       }
+      ts.early = early;
       h->ibuf[5] = early;
     }
     __syncthreads();
@@ -1723,13 +1759,13 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
       if (early == 1) {  // early full fallback (repair_recurrence, cu:535-550)
         const Slot s0 = load_slot(sl + (0));
         const bool resume = frontier_on && s0.frontier_end > 0 && s0.frontier_end <= T;
-        if (resume) { reuse1 += s0.frontier_end; reuse3 += S; }
+        if (resume && tid == 0) { ts.reuse[1] += s0.frontier_end; ts.reuse[3] += S; }
         const DPOut o = dp_interval<K, D, LG>(r, L, 0, T, true, resume ? r.frontier : nullptr,
                                           resume ? s0.frontier_end : 1, nullptr, TRACE_IF_FINITE);
         status = isfinite(o.score) ? 0 : 1;
         objective = o.score;
         early = 2;
-        if (tid == 0) h->ibuf[5] = early;
+        if (tid == 0) { ts.early = early; h->ibuf[5] = early; }
         __syncthreads();
       }
     } else {
@@ -1743,10 +1779,9 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
           if (s.frontier_end > s.a && s.frontier_end <= s.b) {
             resume = true;
             start_t = s.frontier_end;
-            reuse0 += s.frontier_end - s.a;
-            reuse3 += S;
+            if (tid == 0) { ts.reuse[0] += s.frontier_end - s.a; ts.reuse[3] += S; }
           }
-          reuse2 += S;
+          if (tid == 0) ts.reuse[2] += S;
         }
         const DPOut o = dp_interval<K, D, LG>(r, L, s.a, s.b, s.b == T, resume ? fr : nullptr, start_t, fr,
                                           TRACE_ALWAYS);
@@ -1766,7 +1801,7 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
       bool legal = true;
       float total = 0.0f;
       int previous = -1;
-      if (!repairs) { passes = 0; repaired = 0; }
+      if (!repairs) { ts.passes = 0; ts.repaired = 0; }
       for (int k = 0; k < n; ++k) {
         if (repairs && sl[k].a >= sl[k].b) continue;
         const float cost = sl[k].objective;
@@ -1787,7 +1822,7 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
     if (!stitched) {  // fallback_recurrence, cu:552-559
       const Slot s0 = load_slot(sl + (0));
       const bool resume = frontier_on && s0.frontier_end > 0 && s0.frontier_end <= T;
-      if (resume) { reuse1 += s0.frontier_end; reuse3 += S; }
+      if (resume && tid == 0) { ts.reuse[1] += s0.frontier_end; ts.reuse[3] += S; }
       const DPOut o = dp_interval<K, D, LG>(r, L, 0, T, true, resume ? r.frontier : nullptr,
                                         resume ? s0.frontier_end : 1, nullptr, TRACE_IF_FINITE);
       status = isfinite(o.score) ? 0 : 1;
@@ -1799,17 +1834,17 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
     glb(p.status)[rec] = status;
     glb(p.objective)[rec] = objective;
     glb(p.stitched)[rec] = stitched;
-    glb(p.repair_passes)[rec] = passes;
-    glb(p.repaired_frames)[rec] = repaired;
-    glb(p.shortcut_stats)[3 * rec + 0] = sc_accepted;
-    glb(p.shortcut_stats)[3 * rec + 1] = sc_frames;
-    glb(p.shortcut_stats)[3 * rec + 2] = sc_ambiguous;
-    glb(p.routing_stats)[3 * rec + 0] = early;
-    glb(p.routing_stats)[3 * rec + 1] = rejected;
-    glb(p.routing_stats)[3 * rec + 2] = maxprop;
+    glb(p.repair_passes)[rec] = ts.passes;
+    glb(p.repaired_frames)[rec] = ts.repaired;
+    glb(p.shortcut_stats)[3 * rec + 0] = ts.sc_accepted;
+    glb(p.shortcut_stats)[3 * rec + 1] = ts.sc_frames;
+    glb(p.shortcut_stats)[3 * rec + 2] = ts.sc_ambiguous;
+    glb(p.routing_stats)[3 * rec + 0] = ts.early;
+    glb(p.routing_stats)[3 * rec + 1] = ts.rejected;
+    glb(p.routing_stats)[3 * rec + 2] = ts.maxprop;
     if (p.reuse_stats) {
       GLB int64_t* u = glb(p.reuse_stats) + 4 * rec;
-      u[0] = reuse0; u[1] = reuse1; u[2] = reuse2; u[3] = reuse3;
+      u[0] = ts.reuse[0]; u[1] = ts.reuse[1]; u[2] = ts.reuse[2]; u[3] = ts.reuse[3];
     }
   }
 }
