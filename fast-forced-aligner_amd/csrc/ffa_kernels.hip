@@ -954,7 +954,7 @@ __device__ __attribute__((always_inline)) inline TargetLoads issue_targets(const
 
 // Checks and LDS staging of the loaded targets (see stage_targets),
 // specialized for the alphabet form and the keys.
-template <int ALPHABET, bool KEYS>
+template <int ALPHABET, bool KEYS, bool PEEL = false>
 __device__ __attribute__((always_inline)) Staged finish_targets(TargetLoads& t, int V, int blank, int64_t T, int rec,
                                                                  const Params& p, const Lds& L) {
   Header* h = L.h;
@@ -969,8 +969,12 @@ __device__ __attribute__((always_inline)) Staged finish_targets(TargetLoads& t, 
   int repeats = 0;
   uint32_t mask = 0;
   int64_t before = t.before;
-  for (int jb = j0; jb < j1; jb += 8) {
-    if (jb > j0) load_target_batch(t, jb);
+  // PEEL (chunk kernel): the first batch (loaded by issue_targets) is staged
+  // outside the loop. As a loop-carried value it is copied between
+  // registers, and the copy waits for every load in flight, the chunk's rows
+  // included. The other kernels keep the loop form, which their DP loops'
+  // code generation was measured with.
+  auto batch = [&](int jb) {
     int tv[10];  // the staged int16 value of target jb+q: 0 when out of vocabulary, -1 past the end
 #pragma unroll
     for (int q = 0; q < 10; ++q) {
@@ -994,6 +998,41 @@ __device__ __attribute__((always_inline)) Staged finish_targets(TargetLoads& t, 
           if constexpr (ALPHABET == ALPHABET_MASK32) mask |= 1u << (tok & 31);
         }
       }
+    }
+  };
+  if constexpr (PEEL) {
+    if (j0 < j1) batch(j0);
+    for (int jb = j0 + 8; jb < j1; jb += 8) {
+      load_target_batch(t, jb);
+      batch(jb);
+    }
+  } else {
+    for (int jb = j0; jb < j1; jb += 8) {
+      if (jb > j0) load_target_batch(t, jb);
+    int tv[10];  // the staged int16 value of target jb+q: 0 when out of vocabulary, -1 past the end
+#pragma unroll
+    for (int q = 0; q < 10; ++q) {
+      const int64_t tok = t.v[q];
+      tv[q] = jb + q < U ? ((tok < 0 || tok >= V) ? 0 : (int)tok) : -1;
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int j = jb + q;
+      if (j < j1) {
+        const int64_t tok = t.v[q];
+        const bool out = tok < 0 || tok >= V;  // checked as int64 before narrowing (cu:860)
+        oov |= out;
+        bin |= !out && tok == blank;
+        repeats += j > 0 && tok == before;  // cu:861
+        before = tok;
+        L.ytok[j] = (int16_t)tv[q];
+        if constexpr (KEYS) L.key3[j] = (uint16_t)tri_key(tv[q], tv[q + 1], tv[q + 2], ALPHABET == ALPHABET_MASK32);
+        if (!out) {
+          if constexpr (ALPHABET == ALPHABET_BITMAP) atomicOr(&L.bitmap[tok >> 5], 1u << (tok & 31));
+          if constexpr (ALPHABET == ALPHABET_MASK32) mask |= 1u << (tok & 31);
+        }
+      }
+    }
     }
   }
   // sentinel padding after the targets: the placement prefilter reads ahead
@@ -1877,21 +1916,30 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
   const Pending<RecordDesc> pd = issue_uniform(p.desc + rec);
   TargetLoads tl = issue_targets(y, U, p);
   const RecordDesc d = finish_uniform(pd);
+  // Every thread issues the same eight 16-byte loads, clamped to the chunk's
+  // last row and to the row's last quad (chunks off the fast path read their
+  // record's 64-byte descriptor instead; values unused). With a fixed count
+  // the compiler's waits for the targets in the staging below count these
+  // loads exactly instead of waiting for them. Lanes past the chunk's rows
+  // hit lines already requested by lane n-1: no extra HBM traffic.
   float x[32];
+  {
+    const GLB v4f_t* src = fast ? (const GLB v4f_t*)glb(d.emissions + (a + min(tid, n - 1)) * (int64_t)d.vocab)
+                                : (const GLB v4f_t*)glb(p.desc + rec);
+    const int qmax = fast ? quads - 1 : 3;
 #pragma unroll
-  for (int q = 0; q < 32; ++q) x[q] = NEG_INF;
-  if (fast && tid < n) {
-    const GLB v4f_t* src = (const GLB v4f_t*)glb(d.emissions + a * (int64_t)d.vocab) + (int64_t)tid * quads;
-#pragma unroll
-    for (int q = 0; q < 8; ++q)
-      if (q < quads) {
-        const v4f_t v = src[q];
-        x[4 * q] = v.x; x[4 * q + 1] = v.y; x[4 * q + 2] = v.z; x[4 * q + 3] = v.w;
-      }
+    for (int q = 0; q < 8; ++q) {
+      const v4f_t v = src[min(q, qmax)];
+      x[4 * q] = v.x; x[4 * q + 1] = v.y; x[4 * q + 2] = v.z; x[4 * q + 3] = v.w;
+    }
   }
-  const Staged st = fast ? finish_targets<ALPHABET_MASK32, true>(tl, d.vocab, d.blank, d.frames, rec, p, L)
-                   : p.mode == 2 ? finish_targets<ALPHABET_BITMAP, false>(tl, d.vocab, d.blank, d.frames, rec, p, L)
-                                 : finish_targets<ALPHABET_NONE, false>(tl, d.vocab, d.blank, d.frames, rec, p, L);
+  const Staged st = fast ? finish_targets<ALPHABET_MASK32, true, true>(tl, d.vocab, d.blank, d.frames, rec, p, L)
+                   : p.mode == 2 ? finish_targets<ALPHABET_BITMAP, false, true>(tl, d.vocab, d.blank, d.frames, rec, p, L)
+                                 : finish_targets<ALPHABET_NONE, false, true>(tl, d.vocab, d.blank, d.frames, rec, p, L);
+  // columns past V hold -inf (the whole-row maximum below reads all 32)
+#pragma unroll
+  for (int q = 0; q < 8; ++q)
+    if (q >= quads) x[4 * q] = x[4 * q + 1] = x[4 * q + 2] = x[4 * q + 3] = NEG_INF;
   float2 row_st = make_float2(0.0f, 0.0f);
   RowMax whole{NEG_INF, 0, -1};
   if (fast && tid < 128) {
