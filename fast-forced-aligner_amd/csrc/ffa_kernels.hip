@@ -119,6 +119,13 @@ struct TailStats {
   int early, rejected, maxprop, passes;          // routing_stats, repair_passes
 };
 
+struct StageWave {  // one wave's target staging summary (chunk kernel)
+  int flags;      // 1 out-of-vocabulary id, 2 blank id among the targets
+  int repeats;    // adjacent repeats
+  uint32_t mask;  // alphabet mask (V <= 32)
+  int pad;
+};
+
 struct Header {
   float xchg[2][16][2];  // DP neighbour values crossing wave boundaries
   float red_v[16];
@@ -128,9 +135,14 @@ struct Header {
   float term_v[2];
   int ibuf[8];
   float fbuf[4];
-  int stg_f[16];       // per-wave staging flags: 1 out-of-vocabulary id, 2 blank id among the targets
-  int stg_r[16];       // per-wave adjacent-repeat counts
-  uint32_t stg_m[16];  // per-wave alphabet masks (V <= 32)
+  union {
+    struct {
+      int stg_f[16];       // per-wave staging flags: 1 out-of-vocabulary id, 2 blank id among the targets
+      int stg_r[16];       // per-wave adjacent-repeat counts
+      uint32_t stg_m[16];  // per-wave alphabet masks (V <= 32)
+    };
+    StageWave stg[12];     // the same per wave as one record (chunk kernel; 12 >= 10 waves + 2 read ahead)
+  };
   int gbad[2];         // per-wave greedy rejection (fast path)
   int last;            // the record's outputs are written (tail fast path)
   TailStats ts;
@@ -969,70 +981,89 @@ __device__ __attribute__((always_inline)) Staged finish_targets(TargetLoads& t, 
   int repeats = 0;
   uint32_t mask = 0;
   int64_t before = t.before;
+  uint32_t before32 = (uint32_t)before;  // low word of the target before the current one (PEEL)
   // PEEL (chunk kernel): the first batch (loaded by issue_targets) is staged
   // outside the loop. As a loop-carried value it is copied between
   // registers, and the copy waits for every load in flight, the chunk's rows
   // included. The other kernels keep the loop form, which their DP loops'
   // code generation was measured with.
   auto batch = [&](int jb) {
+    // 32-bit checks: a target is in the vocabulary iff its high word is zero
+    // and its low word is below V (the int64 check of cu:860). Repeats
+    // compare low words only; they differ from the int64 comparison only
+    // when a target is out of the vocabulary, and then the status is 3
+    // whatever the count (cu:861, cu:872-873).
     int tv[10];  // the staged int16 value of target jb+q: 0 when out of vocabulary, -1 past the end
+    bool outq[10];
 #pragma unroll
     for (int q = 0; q < 10; ++q) {
-      const int64_t tok = t.v[q];
-      tv[q] = jb + q < U ? ((tok < 0 || tok >= V) ? 0 : (int)tok) : -1;
+      const uint32_t lo = (uint32_t)t.v[q], hi = (uint32_t)((uint64_t)t.v[q] >> 32);
+      outq[q] = (hi | (uint32_t)(lo >= (uint32_t)V)) != 0;
+      tv[q] = jb + q < U ? (outq[q] ? 0 : (int)lo) : -1;
     }
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       const int j = jb + q;
       if (j < j1) {
-        const int64_t tok = t.v[q];
-        const bool out = tok < 0 || tok >= V;  // checked as int64 before narrowing (cu:860)
+        const uint32_t lo = (uint32_t)t.v[q];
+        const bool out = outq[q];
         oov |= out;
-        bin |= !out && tok == blank;
-        repeats += j > 0 && tok == before;  // cu:861
-        before = tok;
+        bin |= !out && (int)lo == blank;
+        repeats += j > 0 && lo == before32;
+        before32 = lo;
         L.ytok[j] = (int16_t)tv[q];
         if constexpr (KEYS) L.key3[j] = (uint16_t)tri_key(tv[q], tv[q + 1], tv[q + 2], ALPHABET == ALPHABET_MASK32);
         if (!out) {
-          if constexpr (ALPHABET == ALPHABET_BITMAP) atomicOr(&L.bitmap[tok >> 5], 1u << (tok & 31));
-          if constexpr (ALPHABET == ALPHABET_MASK32) mask |= 1u << (tok & 31);
+          if constexpr (ALPHABET == ALPHABET_BITMAP) atomicOr(&L.bitmap[lo >> 5], 1u << (lo & 31));
+          if constexpr (ALPHABET == ALPHABET_MASK32) mask |= 1u << (lo & 31);
         }
       }
     }
   };
   if constexpr (PEEL) {
+    // One wait for all of a batch's target loads on every path (they return
+    // together). Otherwise the look-ahead targets that the branches below do
+    // not read stay pending in the compiler's model, and it later waits for
+    // every load in flight, the rows included, before reusing their registers.
+    auto settle = [&] {
+#pragma unroll
+      for (int q = 0; q < 10; ++q) asm volatile("" ::"v"(t.v[q]));
+    };
+    asm volatile("" ::"v"(t.before));
+    settle();
     if (j0 < j1) batch(j0);
     for (int jb = j0 + 8; jb < j1; jb += 8) {
       load_target_batch(t, jb);
+      settle();
       batch(jb);
     }
   } else {
     for (int jb = j0; jb < j1; jb += 8) {
       if (jb > j0) load_target_batch(t, jb);
-    int tv[10];  // the staged int16 value of target jb+q: 0 when out of vocabulary, -1 past the end
+      int tv[10];  // the staged int16 value of target jb+q: 0 when out of vocabulary, -1 past the end
 #pragma unroll
-    for (int q = 0; q < 10; ++q) {
-      const int64_t tok = t.v[q];
-      tv[q] = jb + q < U ? ((tok < 0 || tok >= V) ? 0 : (int)tok) : -1;
-    }
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int j = jb + q;
-      if (j < j1) {
+      for (int q = 0; q < 10; ++q) {
         const int64_t tok = t.v[q];
-        const bool out = tok < 0 || tok >= V;  // checked as int64 before narrowing (cu:860)
-        oov |= out;
-        bin |= !out && tok == blank;
-        repeats += j > 0 && tok == before;  // cu:861
-        before = tok;
-        L.ytok[j] = (int16_t)tv[q];
-        if constexpr (KEYS) L.key3[j] = (uint16_t)tri_key(tv[q], tv[q + 1], tv[q + 2], ALPHABET == ALPHABET_MASK32);
-        if (!out) {
-          if constexpr (ALPHABET == ALPHABET_BITMAP) atomicOr(&L.bitmap[tok >> 5], 1u << (tok & 31));
-          if constexpr (ALPHABET == ALPHABET_MASK32) mask |= 1u << (tok & 31);
+        tv[q] = jb + q < U ? ((tok < 0 || tok >= V) ? 0 : (int)tok) : -1;
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int j = jb + q;
+        if (j < j1) {
+          const int64_t tok = t.v[q];
+          const bool out = tok < 0 || tok >= V;  // checked as int64 before narrowing (cu:860)
+          oov |= out;
+          bin |= !out && tok == blank;
+          repeats += j > 0 && tok == before;  // cu:861
+          before = tok;
+          L.ytok[j] = (int16_t)tv[q];
+          if constexpr (KEYS) L.key3[j] = (uint16_t)tri_key(tv[q], tv[q + 1], tv[q + 2], ALPHABET == ALPHABET_MASK32);
+          if (!out) {
+            if constexpr (ALPHABET == ALPHABET_BITMAP) atomicOr(&L.bitmap[tok >> 5], 1u << (tok & 31));
+            if constexpr (ALPHABET == ALPHABET_MASK32) mask |= 1u << (tok & 31);
+          }
         }
       }
-    }
     }
   }
   // sentinel padding after the targets: the placement prefilter reads ahead
@@ -1041,18 +1072,35 @@ __device__ __attribute__((always_inline)) Staged finish_targets(TargetLoads& t, 
   const int wf = (__ballot(oov) != 0 ? 1 : 0) | (__ballot(bin) != 0 ? 2 : 0);
   const int wr = __builtin_amdgcn_readlane(wave_scan_dpp(repeats), 63);
   const int wm = ALPHABET == ALPHABET_MASK32 ? __builtin_amdgcn_readlane(wave_or_scan_dpp((int)mask), 63) : 0;
-  if (lane == 0) {
-    h->stg_f[wave] = wf;
-    h->stg_r[wave] = wr;
-    h->stg_m[wave] = (uint32_t)wm;
-  }
-  __syncthreads();
   int flags = 0, reps = 0;
   uint32_t m = ALPHABET == ALPHABET_MASK32 ? 1u << blank : 0u;
-  for (int w = 0; w < nw; ++w) {
-    flags |= h->stg_f[w];
-    reps += h->stg_r[w];
-    m |= h->stg_m[w];
+  if constexpr (PEEL) {
+    if (lane == 0) h->stg[wave] = StageWave{wf, wr, (uint32_t)wm, 0};
+    __syncthreads();
+    for (int w0 = 0; w0 < nw; w0 += 4) {  // four records in flight (nw <= 10: reads past nw stay in the array, unused)
+      StageWave sw[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) sw[k] = h->stg[w0 + k];
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (w0 + k < nw) {
+          flags |= sw[k].flags;
+          reps += sw[k].repeats;
+          m |= sw[k].mask;
+        }
+    }
+  } else {
+    if (lane == 0) {
+      h->stg_f[wave] = wf;
+      h->stg_r[wave] = wr;
+      h->stg_m[wave] = (uint32_t)wm;
+    }
+    __syncthreads();
+    for (int w = 0; w < nw; ++w) {
+      flags |= h->stg_f[w];
+      reps += h->stg_r[w];
+      m |= h->stg_m[w];
+    }
   }
   Staged st;
   st.alpha32 = m;
@@ -1937,9 +1985,11 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
                    : p.mode == 2 ? finish_targets<ALPHABET_BITMAP, false, true>(tl, d.vocab, d.blank, d.frames, rec, p, L)
                                  : finish_targets<ALPHABET_NONE, false, true>(tl, d.vocab, d.blank, d.frames, rec, p, L);
   // columns past V hold -inf (the whole-row maximum below reads all 32)
+  if (quads < 8) {
 #pragma unroll
-  for (int q = 0; q < 8; ++q)
-    if (q >= quads) x[4 * q] = x[4 * q + 1] = x[4 * q + 2] = x[4 * q + 3] = NEG_INF;
+    for (int q = 0; q < 8; ++q)
+      if (q >= quads) x[4 * q] = x[4 * q + 1] = x[4 * q + 2] = x[4 * q + 3] = NEG_INF;
+  }
   float2 row_st = make_float2(0.0f, 0.0f);
   RowMax whole{NEG_INF, 0, -1};
   if (fast && tid < 128) {
