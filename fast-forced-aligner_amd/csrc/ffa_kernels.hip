@@ -41,6 +41,8 @@
 namespace ffa {
 
 constexpr float NEG_INF = -INFINITY;
+// 16 bytes of -inf: the chunk kernel's loads of row quads past V read them
+__device__ __align__(16) const float kNegInfQuad[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 constexpr int MAX_H = 512;          // chunk_frames supported by the LDS layout
 constexpr int TAIL_SLOT_CAP = 512;  // record tails with more chunks plan in global memory
 constexpr int YTOK_PAD = 72;        // sentinel entries after the staged targets
@@ -1574,7 +1576,7 @@ __device__ __attribute__((always_inline)) int place_wave(const Lds& L, int g0, i
 // the value, the number of columns equal to it and the last such column.
 struct RowMax {
   float mx;
-  int count, idx;
+  int count, idx;  // idx is meaningful only when count == 1
 };
 
 __device__ __attribute__((always_inline)) inline RowMax row_max(const float (&x)[32], uint32_t cols) {
@@ -1588,14 +1590,12 @@ __device__ __attribute__((always_inline)) inline RowMax row_max(const float (&x)
   for (int w = 8; w >= 1; w >>= 1)
 #pragma unroll
     for (int c = 0; c < w; ++c) t[c] = fmaxf(t[2 * c], t[2 * c + 1]);
-  RowMax r{t[0], 0, -1};
+  // columns equal to the maximum as a bit mask: the count is its population,
+  // the column of a unique maximum its only bit
+  uint32_t eq = 0;
 #pragma unroll
-  for (int c = 0; c < 32; ++c) {
-    const bool e = v[c] == r.mx;
-    r.count += e;
-    r.idx = e ? c : r.idx;
-  }
-  return r;
+  for (int c = 0; c < 32; ++c) eq |= (uint32_t)(v[c] == t[0]) << c;
+  return RowMax{t[0], (int)__popc(eq), 31 - (int)__clz(eq)};
 }
 
 // `whole`: row_max over all 32 register columns (columns past V hold -inf),
@@ -1964,32 +1964,28 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
   const Pending<RecordDesc> pd = issue_uniform(p.desc + rec);
   TargetLoads tl = issue_targets(y, U, p);
   const RecordDesc d = finish_uniform(pd);
-  // Every thread issues the same eight 16-byte loads, clamped to the chunk's
-  // last row and to the row's last quad (chunks off the fast path read their
-  // record's 64-byte descriptor instead; values unused). With a fixed count
-  // the compiler's waits for the targets in the staging below count these
-  // loads exactly instead of waiting for them. Lanes past the chunk's rows
-  // hit lines already requested by lane n-1: no extra HBM traffic.
+  // Every thread issues the same eight 16-byte loads: the row's quads (the
+  // chunk's last row for lanes past it), then -inf for quads past V (chunks
+  // off the fast path read their record's 64-byte descriptor instead; values
+  // unused). With a fixed count the compiler's waits for the targets in the
+  // staging below count these loads exactly instead of waiting for them.
+  // Lanes past the chunk's rows hit lines already requested by lane n-1: no
+  // extra HBM traffic.
   float x[32];
   {
     const GLB v4f_t* src = fast ? (const GLB v4f_t*)glb(d.emissions + (a + min(tid, n - 1)) * (int64_t)d.vocab)
                                 : (const GLB v4f_t*)glb(p.desc + rec);
+    const GLB v4f_t* pad = (const GLB v4f_t*)glb(kNegInfQuad);
     const int qmax = fast ? quads - 1 : 3;
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-      const v4f_t v = src[min(q, qmax)];
+      const v4f_t v = *(q <= qmax ? src + q : pad);
       x[4 * q] = v.x; x[4 * q + 1] = v.y; x[4 * q + 2] = v.z; x[4 * q + 3] = v.w;
     }
   }
   const Staged st = fast ? finish_targets<ALPHABET_MASK32, true, true>(tl, d.vocab, d.blank, d.frames, rec, p, L)
                    : p.mode == 2 ? finish_targets<ALPHABET_BITMAP, false, true>(tl, d.vocab, d.blank, d.frames, rec, p, L)
                                  : finish_targets<ALPHABET_NONE, false, true>(tl, d.vocab, d.blank, d.frames, rec, p, L);
-  // columns past V hold -inf (the whole-row maximum below reads all 32)
-  if (quads < 8) {
-#pragma unroll
-    for (int q = 0; q < 8; ++q)
-      if (q >= quads) x[4 * q] = x[4 * q + 1] = x[4 * q + 2] = x[4 * q + 3] = NEG_INF;
-  }
   float2 row_st = make_float2(0.0f, 0.0f);
   RowMax whole{NEG_INF, 0, -1};
   if (fast && tid < 128) {
