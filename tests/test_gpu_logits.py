@@ -126,12 +126,13 @@ def test_fused_matches_the_oracle(mode):
 @pytest.mark.parametrize("seed", [0, 1])
 def test_fused_random_ragged_batches(mode, seed):
     """Ragged batches over vocabularies that take every read path (greedy fast
-    path, general greedy, LDS-staged and gathered DP), ties, per-record blanks,
-    empty targets and rows off 16-byte alignment."""
+    path with and without quads past V, general greedy, LDS-staged and
+    gathered DP), ties, per-record blanks, empty targets and rows off 16-byte
+    alignment."""
     rng = np.random.default_rng(300 + seed)
     logits, targets, blanks = [], [], []
     for i in range(20):
-        V = int(rng.choice([3, 6, 32, 40, 300]))
+        V = int(rng.choice([3, 6, 12, 28, 32, 40, 300]))
         blank = int(rng.integers(0, V))
         vocab = np.array([v for v in range(V) if v != blank])
         U = int(rng.integers(0, 50))

@@ -91,6 +91,36 @@ def test_random_ragged_batches(mode, seed):
     compare(es, ys, blanks, mode=mode, where=f"seed{seed}")
 
 
+@pytest.mark.parametrize("mode", ["conventional", "optimized"])
+def test_fast_path_narrow_vocabularies(mode):
+    """The chunk kernel's register fast path (V <= 32, V % 4 == 0) for every V
+    it takes: rows narrower than 32 columns leave quads past V, which must read
+    as -inf. Targets sit near the top of the vocabulary, so the last real
+    column often holds a row's maximum; integer rows add ties."""
+    rng = np.random.default_rng(404)
+    es, ys, blanks = [], [], []
+    for i in range(24):
+        V = (4, 8, 12, 16, 20, 24, 28, 32)[i % 8]
+        blank = 0 if i % 3 else V - 1
+        vocab = np.array([v for v in range(V) if v != blank])
+        U = int(rng.integers(1, 80))
+        y = rng.choice(vocab[-3:] if i % 2 else vocab, U).astype(np.int64)
+        R = int((y[1:] == y[:-1]).sum())
+        T = int(rng.integers(U + R, U + R + 500))
+        if i % 4 == 3:
+            e = rng.integers(-3, 1, (T, V)).astype(np.float32)
+        else:
+            e = workloads.peaky(rng, y, T, V, blank)
+        es.append(e)
+        ys.append(y)
+        blanks.append(blank)
+    print(f"narrow vocabularies {mode}", flush=True)
+    got = compare(es, ys, blanks, mode=mode, where="narrow-V")
+    if mode == "optimized":
+        peaky = [i for i in range(24) if i % 4 != 3]
+        assert (got["shortcut_stats"][peaky, 0] > 0).any()  # the fast path accepted chunks
+
+
 @pytest.mark.parametrize("config", ["c2", "c4", "c5"])
 @pytest.mark.parametrize("mode", ["conventional", "optimized"])
 def test_config_parity(config, mode):
