@@ -39,6 +39,7 @@ def hip_runtime():
     lib.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
     lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
     lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+    lib.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
     return lib
 
 
@@ -72,6 +73,39 @@ def measure(capi_lib, hip, call, steps, warmup):
         hip.hipEventDestroy(a)
         hip.hipEventDestroy(b)
     return elapsed / steps, sum(kernel_ms) / len(kernel_ms), result
+
+
+def launch_floor(capi_lib, hip, workgroups, steps):
+    """Mean duration, timed like the dominant kernel (one timing-only event
+    pair per launch, launches back to back on the current stream), of a kernel
+    that does nothing, launched with the dominant kernel's workgroup count: the
+    fixed cost of one dispatch under this timing method, beneath every
+    measured kernel duration (the block size does not change it)."""
+    import torch
+
+    stream = torch.cuda.current_stream().cuda_stream
+    pairs = []
+    for _ in range(steps):
+        a, b = ctypes.c_void_p(), ctypes.c_void_p()
+        assert hip.hipEventCreateWithFlags(ctypes.byref(a), HIP_EVENT_DISABLE_SYSTEM_FENCE) == 0
+        assert hip.hipEventCreateWithFlags(ctypes.byref(b), HIP_EVENT_DISABLE_SYSTEM_FENCE) == 0
+        pairs.append((a, b))
+    for _ in range(10):
+        assert capi_lib.ffa_launch_floor(workgroups, 256, stream) == 0
+    torch.cuda.synchronize()
+    for a, b in pairs:
+        assert hip.hipEventRecord(a, stream) == 0
+        assert capi_lib.ffa_launch_floor(workgroups, 256, stream) == 0
+        assert hip.hipEventRecord(b, stream) == 0
+    torch.cuda.synchronize()
+    total = 0.0
+    for a, b in pairs:
+        ms = ctypes.c_float()
+        assert hip.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+        total += ms.value
+        hip.hipEventDestroy(a)
+        hip.hipEventDestroy(b)
+    return total / steps * 1e3
 
 
 def measured_traffic(config, mode, kernel):
@@ -335,6 +369,13 @@ def main() -> int:
                      "traffic": measured_traffic(args.config, args.mode, kernel_name),
                      "kernel": kernel_name, "kernel_us": kernel_ms * 1e3, "algorithmic_bytes": min_bytes},
     }
+    # the same timing of an empty kernel with the dominant kernel's workgroup
+    # count, and the fraction a kernel of exactly that duration would reach
+    groups = 8 * ((sum((e.shape[0] + 127) // 128 for e in batch.emissions) + 7) // 8) \
+        if args.mode == "optimized" else len(es)
+    floor_us = launch_floor(capi_lib, hip, groups, args.steps)
+    line["roofline"]["launch_floor_us"] = floor_us
+    line["roofline"]["frac_ceiling"] = min_bytes / (floor_us * 1e-6) / 1e9 / HBM_PEAK_GBS
     if not args.no_conventional and args.mode == "optimized":
         c_step, c_kernel_ms, c_achieved, _ = figures("conventional", max(10, args.steps // 10), 3)
         line["conventional"] = {"ms_per_step": c_step * 1e3, "frames_per_s": batch.frames / c_step,

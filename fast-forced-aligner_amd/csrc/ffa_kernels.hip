@@ -2239,6 +2239,11 @@ __global__ void __launch_bounds__(256) log_softmax_kernel(const ffa_logits_recor
   for (int i = threadIdx.x; i < total; i += blockDim.x) dst[i] = lsm(src[i], st[i / V]);
 }
 
+// Measurement: a kernel that does nothing, launched with a given shape, so
+// that the fixed cost of one dispatch as seen by a timing method (HIP events,
+// a profiler) can be set beside the kernels' durations.
+__global__ void empty_kernel() {}
+
 __global__ void __launch_bounds__(1024) validity_kernel(const int64_t* desc, uint8_t* valid) {
   const int rec = blockIdx.x;
   const GLB float* values = (const GLB float*)(glb(desc)[2 * rec]);
@@ -2339,6 +2344,14 @@ const char* ffa_last_error(void) { return g_error.c_str(); }
 int ffa_profile_next_launch(hipEvent_t start, hipEvent_t stop) {
   g_profile_start = start;
   g_profile_stop = stop;
+  return FFA_OK;
+}
+
+int ffa_launch_floor(int32_t workgroups, int32_t threads, hipStream_t stream) {
+  if (workgroups <= 0 || threads <= 0 || threads > 1024) return fail(FFA_E_INVALID, "workgroups > 0, threads 1..1024");
+  hipLaunchKernelGGL(ffa::empty_kernel, dim3((unsigned)workgroups), dim3((unsigned)threads), 0, stream);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(FFA_E_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
   return FFA_OK;
 }
 

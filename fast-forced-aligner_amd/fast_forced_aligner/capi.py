@@ -20,7 +20,7 @@ FFA_MAX_STATES = 20479
 
 EXPORTED = ("ffa_default_options", "ffa_align_plan_batch", "ffa_align_describe", "ffa_align_launch",
             "ffa_emission_validity_launch", "ffa_token_spans_launch", "ffa_log_softmax_launch", "ffa_last_error",
-            "ffa_profile_next_launch")
+            "ffa_profile_next_launch", "ffa_launch_floor")
 
 
 class SpanRecord(ctypes.Structure):
@@ -79,6 +79,8 @@ def load(path: Path | str = HIP_LIBRARY) -> ctypes.CDLL:
     lib.ffa_last_error.argtypes = []
     lib.ffa_profile_next_launch.restype = ctypes.c_int
     lib.ffa_profile_next_launch.argtypes = [p, p]
+    lib.ffa_launch_floor.restype = ctypes.c_int
+    lib.ffa_launch_floor.argtypes = [ctypes.c_int32, ctypes.c_int32, p]
     lib.ffa_token_spans_launch.restype = ctypes.c_int
     lib.ffa_token_spans_launch.argtypes = [p, ctypes.c_int64, p, p, p, p]
     lib.ffa_log_softmax_launch.restype = ctypes.c_int

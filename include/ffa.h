@@ -182,6 +182,12 @@ const char* ffa_last_error(void);
  * after it. Passing NULL events disarms. */
 int ffa_profile_next_launch(hipEvent_t start, hipEvent_t stop);
 
+/* Measurement hook (no counterpart in the reference). Launches a kernel that
+ * does nothing with `workgroups` x `threads` (1..1024) on `stream`: timed like
+ * the dominant kernel, it gives the fixed cost of one dispatch under that
+ * timing method, the floor beneath every kernel's measured duration. */
+int ffa_launch_floor(int32_t workgroups, int32_t threads, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

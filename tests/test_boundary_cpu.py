@@ -241,3 +241,9 @@ def test_logits_entry_points_check_arguments_on_the_host(lib):
         ffa.log_softmax([])
     with pytest.raises(ValueError, match="contiguous CUDA"):
         ffa.log_softmax([e])
+
+
+@pytest.mark.parametrize("workgroups, threads", [(0, 64), (-1, 64), (8, 0), (8, 1025)])
+def test_launch_floor_checks_its_shape_on_the_host(lib, workgroups, threads):
+    assert lib.ffa_launch_floor(workgroups, threads, None) == -1
+    assert "threads 1..1024" in lib.ffa_last_error().decode()
