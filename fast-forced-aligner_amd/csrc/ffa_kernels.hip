@@ -603,8 +603,11 @@ struct Waves {
 };
 
 // LG: logits input (emission reads pass through lsm with r.st); a template
-// parameter so that the log-probability build carries none of it.
-template <int K, int D, bool LG>
+// parameter so that the log-probability build carries none of it. BYREC (the
+// chunk and tail kernels): the K = 4 loops pick the one-wave form by the
+// record's width, not the workgroup's (the conventional kernel keeps the
+// workgroup test: its longest record sets its time and takes the same loop).
+template <int K, int D, bool LG, bool BYREC = true>
 __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const Lds& L, int64_t a, int64_t b, bool record_end,
                              const GLB float* resume_from, int64_t start_t, GLB float* save_frontier, int trace) {
   using Bits = typename BitsT<K>::type;
@@ -702,6 +705,12 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
     }
   };
   const int64_t last = b - 1;
+  // A record whose states all sit in wave 0 (at most 64 threads' worth) runs
+  // the one-wave loop even in a wider workgroup: the other waves hold only
+  // states past S, which nothing reads, and wave 0 receives from no wave, so
+  // no exchange or barrier is needed per frame (the per-block barriers of the
+  // staged path are still met by every wave).
+  const bool multi = nwaves > 1 && (!BYREC || r.S > 64 * K);
   if (L.eblk && V <= EBLK_COLS) {
     // Emission rows staged in LDS, one block of F frames at a time (the block's
     // rows are one contiguous span of F*V floats in HBM, so every thread loads
@@ -762,7 +771,7 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
       // (K >= 8 only comes with more than 128 threads: always several waves;
       // K = 32 keeps a plain loop, which spills less in the chunk and tail kernels)
       if constexpr (K == 4) {
-        if (nwaves > 1) frames(Waves<1>{});
+        if (multi) frames(Waves<1>{});
         else frames(Waves<0>{});
       } else if constexpr (K == 32) {
         for (int f = 0; f < nf; ++f) {
@@ -824,7 +833,7 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
       }
   };
   if constexpr (K == 4) {
-    if (nwaves > 1) ring(Waves<1>{});
+    if (multi) ring(Waves<1>{});
     else ring(Waves<0>{});
   } else if constexpr (K == 32) {  // plain loop (spills less in the chunk and tail kernels)
     int64_t t0 = start_t;
@@ -1679,7 +1688,7 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) conventional_kernel(Param
     write_failed(r, 0, r.T);
     return;
   }
-  const DPOut o = dp_interval<K, D, LG>(r, L, 0, r.T, true, nullptr, 1, nullptr, TRACE_IF_FINITE);
+  const DPOut o = dp_interval<K, D, LG, false>(r, L, 0, r.T, true, nullptr, 1, nullptr, TRACE_IF_FINITE);
   const bool ok = isfinite(o.score);
   if (threadIdx.x == 0) { glb(p.status)[rec] = ok ? 0 : 1; glb(p.objective)[rec] = o.score; }  // cu:507-510
   if (!ok) write_failed(r, 0, r.T);
