@@ -268,3 +268,17 @@ def test_emission_validity_scan():
     mask = ffa.emission_validity([torch.from_numpy(e).to(DEV) for e in es])
     assert mask.dtype == torch.bool
     assert mask.cpu().tolist() == [O.emission_valid(e) for e in es] == [True, False, False, True]
+
+
+def test_launch_floor_hook_runs_on_the_current_stream():
+    """The measurement hook launches its empty kernel without error and leaves
+    the stream usable; an alignment enqueued after it is unaffected."""
+    lib = capi.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    for shape in ((1, 64), (568, 192), (1024, 256)):
+        assert lib.ffa_launch_floor(shape[0], shape[1], stream) == 0, lib.ffa_last_error()
+    b = workloads.c1()
+    got = run_gpu(b.emissions, b.targets, mode="optimized")
+    torch.cuda.synchronize()
+    want = O.align(b.emissions, b.targets, blank_id=0, mode="optimized")
+    assert_same(got, want, where="after-floor ")
