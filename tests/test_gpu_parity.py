@@ -282,3 +282,32 @@ def test_launch_floor_hook_runs_on_the_current_stream():
     torch.cuda.synchronize()
     want = O.align(b.emissions, b.targets, blank_id=0, mode="optimized")
     assert_same(got, want, where="after-floor ")
+
+
+@pytest.mark.parametrize("mode", ["conventional", "optimized"])
+def test_dp_wave_selection_boundaries(mode):
+    """Records on both sides of the one-wave DP loop's limit (S = 255 and 257
+    states with K = 4 states per thread, i.e. 64 and 65 threads) in a batch
+    whose widest record (S = 1023) makes four-wave workgroups: the chunk DP,
+    the repairs and the fallback of optimized mode and the conventional DP
+    must agree with the oracle whichever loop each record takes."""
+    rng = np.random.default_rng(2560)
+    es, ys = [], []
+    for U, kind in [(127, "ties"), (128, "ties"), (127, "peaky"), (128, "flat"), (256, "ties"), (511, "peaky"),
+                    (130, "flat"), (64, "ties")]:
+        V = 32
+        y = rng.integers(1, V, U).astype(np.int64)
+        R = int((y[1:] == y[:-1]).sum())
+        T = int(rng.integers(U + R + 2, U + R + 600))
+        if kind == "ties":
+            e = rng.integers(-3, 1, (T, V)).astype(np.float32)
+        elif kind == "flat":
+            e = np.log(rng.dirichlet(np.ones(V) * 50, T)).astype(np.float32)
+        else:
+            e = workloads.peaky(rng, y, T, V, 0)
+        es.append(e)
+        ys.append(y)
+    print(f"dp wave boundaries {mode}", flush=True)
+    got = compare(es, ys, mode=mode, where="wave-boundary")
+    if mode == "optimized":  # the tie and flat records take chunk DPs and repair rounds
+        assert (got["repair_passes"] > 0).sum() >= 4 and (got["shortcut_stats"][:, 0] == 0).sum() >= 5
