@@ -540,6 +540,10 @@ struct BitsT { using type = uint32_t; };
 template <>
 struct BitsT<32> { using type = uint64_t; };
 
+// Write-only target of the DP's backpointer stores from threads past a
+// record's states (lane-indexed: at most 64 lanes x 8 bytes); never read.
+__device__ uint32_t g_bp_sink[128];
+
 template <int K>
 __device__ inline void store_row(GLB uint32_t* row, int tid, typename BitsT<K>::type bits) {
   if constexpr (K == 32) {
@@ -633,6 +637,22 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
   const GLB float* e = r.e;
   const int64_t V = r.V;
   GLB uint32_t* bp = r.bp;
+  // Exchange and store forms per state width, each the fastest measured
+  // (the K = 8/16 loops slow down by 5% with any of the other forms, even
+  // with only the slot numbering changed):
+  //   K = 4:  exchanged value as the lane-0 fill of the DPP shift, sink store
+  //           (threads without states store their unused frame bits into a
+  //           sink instead of branching around the store every frame);
+  //   K = 32: DPP shifts independent of the exchange read, lane 0 selects it
+  //           afterwards, sink store;
+  //   K = 8, 16: lane 0 of waves past the first reads in a branch, stores
+  //           only from threads with states.
+  // Forms 1 and 2 read every lane's own wave slot: wave w's last states go
+  // to slot w + 1 and slot 0 holds -inf for wave 0 (nothing writes it); the
+  // branch form keeps wave w in slot w.
+  constexpr int kRead = K == 4 ? 1 : K == 32 ? 2 : 0;
+  constexpr bool kSink = kRead != 0;
+  constexpr int kSlot = kRead != 0 ? 1 : 0;
   if (resume_from) {
 #pragma unroll
     for (int k = 0; k < K; ++k) al[k] = (s0 + k < S) ? resume_from[s0 + k] : NEG_INF;
@@ -648,10 +668,12 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
     if (active) store_row<K>(bp + a * (int64_t)r.stride, tid, (Bits)0);  // cu:410
     start_t = a + 1;
   }
-  if (nwaves > 1) {
+  if (nwaves > 1) {  // at most 10 waves: slots 0..10 of 16
+    if constexpr (kSlot != 0)
+      if (tid < 4) h->xchg[tid >> 1][0][tid & 1] = NEG_INF;
     if (lane == 63) {
-      h->xchg[(start_t - 1) & 1][wave][0] = al[K - 2];
-      h->xchg[(start_t - 1) & 1][wave][1] = al[K - 1];
+      h->xchg[(start_t - 1) & 1][wave + kSlot][0] = al[K - 2];
+      h->xchg[(start_t - 1) & 1][wave + kSlot][1] = al[K - 1];
     }
     __syncthreads();
   }
@@ -668,12 +690,33 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
     // multi-wave loops for K <= 16 exchange just that value across waves (the
     // other loops keep both, which measured faster for them).
     constexpr bool kOneUp = K <= 16 && WM == 1;
-    float up1 = wave_shr1(al[K - 1], NEG_INF);
-    float up2 = kOneUp ? up1 : wave_shr1(al[K - 2], NEG_INF);
-    if (M && lane == 0 && wave > 0) {
-      const int par = (int)((t - 1) & 1);
-      if constexpr (!kOneUp) up2 = h->xchg[par][wave - 1][0];
-      up1 = h->xchg[par][wave - 1][1];
+    float up1, up2;
+    if constexpr (kRead == 1) {  // exchange value as the shift's lane-0 fill
+      float fill1 = NEG_INF, fill2 = NEG_INF;
+      if (M) {
+        const int par = (int)((t - 1) & 1);
+        fill1 = h->xchg[par][wave][1];
+        if constexpr (!kOneUp) fill2 = h->xchg[par][wave][0];
+      }
+      up1 = wave_shr1(al[K - 1], fill1);
+      up2 = kOneUp ? up1 : wave_shr1(al[K - 2], fill2);
+    } else if constexpr (kRead == 2) {  // shifts independent of the read; lane 0 selects it
+      up1 = wave_shr1(al[K - 1], NEG_INF);
+      up2 = kOneUp ? up1 : wave_shr1(al[K - 2], NEG_INF);
+      if (M) {
+        const int par = (int)((t - 1) & 1);
+        const float x1 = h->xchg[par][wave][1];
+        if constexpr (!kOneUp) up2 = lane == 0 ? h->xchg[par][wave][0] : up2;
+        up1 = lane == 0 ? x1 : up1;
+      }
+    } else {  // lane 0 of waves past the first reads in a branch
+      up1 = wave_shr1(al[K - 1], NEG_INF);
+      up2 = kOneUp ? up1 : wave_shr1(al[K - 2], NEG_INF);
+      if (M && lane == 0 && wave > 0) {
+        const int par = (int)((t - 1) & 1);
+        if constexpr (!kOneUp) up2 = h->xchg[par][wave - 1][0];
+        up1 = h->xchg[par][wave - 1][1];
+      }
     }
     Bits bits = 0;
 #pragma unroll
@@ -695,11 +738,14 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
       al[k] = best + evk[k];
       bits |= j << (2 * k);
     }
-    if (active) store_row<K>(bp + t * (int64_t)r.stride, tid, bits);
+    if constexpr (kSink)
+      store_row<K>((active ? bp : glb(g_bp_sink)) + t * (active ? (int64_t)r.stride : 0), active ? tid : lane, bits);
+    else if (active)
+      store_row<K>(bp + t * (int64_t)r.stride, tid, bits);
     if (M) {
       if (lane == 63) {
-        if constexpr (!kOneUp) h->xchg[t & 1][wave][0] = al[K - 2];
-        h->xchg[t & 1][wave][1] = al[K - 1];
+        if constexpr (!kOneUp) h->xchg[t & 1][wave + kSlot][0] = al[K - 2];
+        h->xchg[t & 1][wave + kSlot][1] = al[K - 1];
       }
       __syncthreads();
     }
