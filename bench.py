@@ -8,7 +8,8 @@ kernels); K steps run back to back with no host synchronization in between.
 
 Prints one JSON line: aligned frames/s as ``value``, DP cells/s, the dominant
 kernel's HBM roofline fraction (kernel duration from HIP events recorded on the
-launch stream around that kernel in every timed step), the same figures for
+launch stream around that kernel in each of a second pass of K steps, kept out
+of the throughput pass because the event records are host work), the same figures for
 conventional mode, and a CPU baseline (the oracle's conventional DP on the
 host cores, a bounded sample of the same batch).
 """
@@ -44,13 +45,22 @@ def hip_runtime():
 
 
 def measure(capi_lib, hip, call, steps, warmup):
-    """Pipelined wall time per call of `call` (an align entry) and the average
-    duration of its dominant kernel from the armed HIP events."""
+    """Pipelined wall time per call of `call` (an align entry): `steps` calls
+    back to back with nothing else on the host between them, bracketed by two
+    synchronizations. Then the average duration of its dominant kernel, from
+    timing-only HIP events armed around that kernel in a second pass of
+    `steps` calls (the event records are host work of their own, so they stay
+    out of the throughput pass)."""
     import torch
 
     for _ in range(warmup):
         call()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        call()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
     starts, stops = [], []
     for _ in range(steps):
         a, b = ctypes.c_void_p(), ctypes.c_void_p()
@@ -59,12 +69,10 @@ def measure(capi_lib, hip, call, steps, warmup):
         starts.append(a)
         stops.append(b)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
     for i in range(steps):
         capi_lib.ffa_profile_next_launch(starts[i], stops[i])
         result = call()
     torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
     kernel_ms = []
     for a, b in zip(starts, stops):
         ms = ctypes.c_float()

@@ -643,14 +643,17 @@ __device__ __attribute__((always_inline)) DPOut dp_interval(const Rec& r, const 
   //   K = 4:  exchanged value as the lane-0 fill of the DPP shift, sink store
   //           (threads without states store their unused frame bits into a
   //           sink instead of branching around the store every frame);
-  //   K = 32: DPP shifts independent of the exchange read, lane 0 selects it
-  //           afterwards, sink store;
-  //   K = 8, 16: lane 0 of waves past the first reads in a branch, stores
-  //           only from threads with states.
+  //   K = 32, conventional kernel: DPP shifts independent of the exchange
+  //           read, lane 0 selects it afterwards, sink store;
+  //   K = 8, 16, and K = 32 in the chunk and tail kernels: lane 0 of waves
+  //           past the first reads in a branch, stores only from threads with
+  //           states (K = 32's chunk and tail kernels run at the register
+  //           limit; the other forms move spills into their frame loops and
+  //           made C3 optimized 55% slower).
   // Forms 1 and 2 read every lane's own wave slot: wave w's last states go
   // to slot w + 1 and slot 0 holds -inf for wave 0 (nothing writes it); the
   // branch form keeps wave w in slot w.
-  constexpr int kRead = K == 4 ? 1 : K == 32 ? 2 : 0;
+  constexpr int kRead = K == 4 ? 1 : (K == 32 && !BYREC) ? 2 : 0;
   constexpr bool kSink = kRead != 0;
   constexpr int kSlot = kRead != 0 ? 1 : 0;
   if (resume_from) {
