@@ -311,3 +311,37 @@ def test_dp_wave_selection_boundaries(mode):
     got = compare(es, ys, mode=mode, where="wave-boundary")
     if mode == "optimized":  # the tie and flat records take chunk DPs and repair rounds
         assert (got["repair_passes"] > 0).sum() >= 4 and (got["shortcut_stats"][:, 0] == 0).sum() >= 5
+
+
+@pytest.mark.parametrize("mode", ["conventional", "optimized"])
+@pytest.mark.parametrize("case", ["k16", "gather_k4", "gather_k8"])
+def test_state_widths_and_gathered_rows(mode, case):
+    """The DP at every state width and read path the configs leave out: K = 16
+    (transcripts of 1,024 to 2,047 tokens, three-wave workgroups) with staged
+    rows, and the gathered-row path (V > 64) in multi-wave workgroups at K = 4
+    and K = 8, whose cross-wave exchange differs from the staged path's loops.
+    Tie, flat and peaky rows make optimized mode run chunk DPs, repairs and
+    fallbacks as well as greedy shortcuts."""
+    rng = np.random.default_rng({"k16": 1600, "gather_k4": 1601, "gather_k8": 1602}[case])
+    V, widest = {"k16": (32, 1300), "gather_k4": (100, 200), "gather_k8": (80, 600)}[case]
+    es, ys = [], []
+    for U, kind in [(widest, "peaky"), (widest - 7, "ties"), (widest // 2, "flat"), (widest // 3, "peaky"),
+                    (40, "ties")]:
+        y = rng.integers(1, V, U).astype(np.int64)
+        R = int((y[1:] == y[:-1]).sum())
+        T = int(rng.integers(U + R + 2, 2 * (U + R) + 300))
+        if kind == "ties":
+            e = rng.integers(-3, 1, (T, V)).astype(np.float32)
+        elif kind == "flat":
+            e = np.log(rng.dirichlet(np.ones(V) * 50, T)).astype(np.float32)
+        else:
+            e = workloads.peaky(rng, y, T, V, 0)
+        es.append(e)
+        ys.append(y)
+    S = 2 * widest + 1
+    K = 4
+    while K < 32 and (S + K - 1) // K > 256:
+        K *= 2
+    assert K == {"k16": 16, "gather_k4": 4, "gather_k8": 8}[case] and (S + K - 1) // K > 64  # several waves
+    print(f"state widths {case} {mode}", flush=True)
+    compare(es, ys, mode=mode, where=case)
