@@ -6,12 +6,14 @@ peaky synthetic emissions), optimized mode, inputs resident in HBM. A step is
 one ``align`` call over the whole batch (host preparation, descriptor upload,
 kernels); K steps run back to back with no host synchronization in between.
 
-Prints one JSON line: aligned frames/s as ``value``, DP cells/s, the dominant
-kernel's HBM roofline fraction (kernel duration from HIP events recorded on the
-launch stream around that kernel in each of a second pass of K steps, kept out
-of the throughput pass because the event records are host work), the same figures for
-conventional mode, and a CPU baseline (the oracle's conventional DP on the
-host cores, a bounded sample of the same batch).
+Prints one JSON line: aligned frames/s as ``value`` (the median of five passes
+of K steps), DP cells/s, the dominant kernel's HBM roofline fraction (kernel
+duration from HIP events recorded on the launch stream around that kernel in
+five further passes of K steps, kept out of the throughput passes because the
+event records are host work), the same figures for conventional mode, and a CPU
+baseline (conventional-mode alignment on the host cores, a bounded sample of
+the same batch: the reference's own CPU comparator where it was built, else the
+C oracle).
 """
 from __future__ import annotations
 
@@ -44,43 +46,53 @@ def hip_runtime():
     return lib
 
 
-def measure(capi_lib, hip, call, steps, warmup):
-    """Pipelined wall time per call of `call` (an align entry): `steps` calls
-    back to back with nothing else on the host between them, bracketed by two
-    synchronizations. Then the average duration of its dominant kernel, from
-    timing-only HIP events armed around that kernel in a second pass of
-    `steps` calls (the event records are host work of their own, so they stay
-    out of the throughput pass)."""
+def measure(capi_lib, hip, call, steps, warmup, repeats=5):
+    """Pipelined wall time per call of `call` (an align entry): `repeats`
+    passes of `steps` calls back to back with nothing else on the host between
+    them, each pass bracketed by two synchronizations; the median pass. Then
+    the average duration of its dominant kernel, from timing-only HIP events
+    armed around that kernel in `repeats` further passes of `steps` calls (the
+    event records are host work of their own, so they stay out of the
+    throughput passes); the median pass."""
+    import statistics
+
     import torch
 
     for _ in range(warmup):
         call()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        call()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    starts, stops = [], []
-    for _ in range(steps):
-        a, b = ctypes.c_void_p(), ctypes.c_void_p()
-        assert hip.hipEventCreateWithFlags(ctypes.byref(a), HIP_EVENT_DISABLE_SYSTEM_FENCE) == 0
-        assert hip.hipEventCreateWithFlags(ctypes.byref(b), HIP_EVENT_DISABLE_SYSTEM_FENCE) == 0
-        starts.append(a)
-        stops.append(b)
-    torch.cuda.synchronize()
-    for i in range(steps):
-        capi_lib.ffa_profile_next_launch(starts[i], stops[i])
-        result = call()
-    torch.cuda.synchronize()
-    kernel_ms = []
-    for a, b in zip(starts, stops):
-        ms = ctypes.c_float()
-        assert hip.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
-        kernel_ms.append(ms.value)
-        hip.hipEventDestroy(a)
-        hip.hipEventDestroy(b)
-    return elapsed / steps, sum(kernel_ms) / len(kernel_ms), result
+    passes = []
+    for _ in range(repeats):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            call()
+        torch.cuda.synchronize()
+        passes.append((time.perf_counter() - t0) / steps)
+    kernel_passes = []
+    result = None
+    for _ in range(repeats):
+        starts, stops = [], []
+        for _ in range(steps):
+            a, b = ctypes.c_void_p(), ctypes.c_void_p()
+            assert hip.hipEventCreateWithFlags(ctypes.byref(a), HIP_EVENT_DISABLE_SYSTEM_FENCE) == 0
+            assert hip.hipEventCreateWithFlags(ctypes.byref(b), HIP_EVENT_DISABLE_SYSTEM_FENCE) == 0
+            starts.append(a)
+            stops.append(b)
+        torch.cuda.synchronize()
+        for i in range(steps):
+            capi_lib.ffa_profile_next_launch(starts[i], stops[i])
+            result = call()
+        torch.cuda.synchronize()
+        kernel_ms = []
+        for a, b in zip(starts, stops):
+            ms = ctypes.c_float()
+            assert hip.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+            kernel_ms.append(ms.value)
+            hip.hipEventDestroy(a)
+            hip.hipEventDestroy(b)
+        kernel_passes.append(sum(kernel_ms) / len(kernel_ms))
+    return statistics.median(passes), statistics.median(kernel_passes), result
 
 
 def launch_floor(capi_lib, hip, workgroups, steps):
@@ -200,9 +212,29 @@ def logits_figures(ffa, capi_lib, hip, config, mode, steps=100):
             "parity_vs_materialized": bool(parity)}
 
 
+def cpu_model():
+    """The host CPU's model name from /proc/cpuinfo (None where unreadable)."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(batch, seconds=10.0):
-    """The oracle's conventional DP (same recurrence and tie rule as the
-    reference's conventional mode) on host threads, one record per task."""
+    """Conventional-mode CPU alignment of the same batch on the host cores, one
+    record per task, repeated for about `seconds`. Prefers the reference's own
+    CPU comparator (benchmarks/patches/cpu_corrected.cpp, built from the
+    reference sources into oracle/_ref; same fp32 recurrence and tie rule as the
+    reference's conventional mode; run on a thread pool as the reference's
+    adapter does, benchmarks/adapters/cpp.py:86-117) when it was built and the
+    batch lies in its domain; otherwise the C oracle's conventional DP."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import numpy as np
+
     from oracle import oracle
 
     try:
@@ -210,17 +242,39 @@ def cpu_baseline(batch, seconds=10.0):
     except AttributeError:
         cores = os.cpu_count() or 1
     cores = max(1, min(cores, 16))
+    ref = oracle.reference_comparator()
+    in_domain = all(y.size > 0 and e.shape[0] >= y.size + int((y[1:] == y[:-1]).sum()) + 2
+                    for e, y in zip(batch.emissions, batch.targets))
+    if ref is not None and in_domain:
+        items = [(np.ascontiguousarray(e[None]), np.ascontiguousarray(y[None])) for e, y in
+                 zip(batch.emissions, batch.targets)]
+        pool = ThreadPoolExecutor(max_workers=cores)
+
+        def run():
+            list(pool.map(lambda item: ref.forced_align(item[0], item[1], 0), items))
+
+        kind, what = "reference", "the reference's CPU comparator (cpu_corrected.cpp, oracle/_ref)"
+    else:
+        pool = None
+
+        def run():
+            oracle.align(batch.emissions, batch.targets, mode="conventional", threads=cores)
+
+        kind, what = "port", "the C oracle's conventional DP"
+    run()  # warm caches and the thread pool outside the timed region
     reps, t0 = 0, time.perf_counter()
     while True:
-        oracle.align(batch.emissions, batch.targets, mode="conventional", threads=cores)
+        run()
         reps += 1
         if time.perf_counter() - t0 >= seconds:
             break
     elapsed = time.perf_counter() - t0
-    return {"value": batch.frames * reps / elapsed, "unit": "aligned frames/s", "cores": cores, "kind": "port",
-            "dp_cells_per_s": batch.cells * reps / elapsed,
-            "sample": f"{batch.name} full batch x{reps} ({elapsed:.1f} s), conventional DP, C oracle, "
-                      f"one record per thread"}
+    if pool is not None:
+        pool.shutdown()
+    return {"value": batch.frames * reps / elapsed, "unit": "aligned frames/s", "cores": cores, "kind": kind,
+            "cpu_model": cpu_model(), "dp_cells_per_s": batch.cells * reps / elapsed,
+            "sample": f"{batch.name} full batch x{reps} ({elapsed:.1f} s), conventional DP, {what}, "
+                      f"one record per task on {cores} threads"}
 
 
 def matrix(path: str) -> int:
@@ -268,13 +322,7 @@ def matrix(path: str) -> int:
                     singles.append(time.perf_counter() - t0)
                 single = statistics.median(singles)
                 k = max(3, min(100, int(0.3 / single)))
-                piped, kernels = [], []
-                for _ in range(5):
-                    step_s, kernel_ms, result = measure(capi_lib, hip, call, k, 2)
-                    piped.append(step_s)
-                    kernels.append(kernel_ms)
-                step = statistics.median(piped)
-                kernel_ms = statistics.median(kernels)
+                step, kernel_ms, result = measure(capi_lib, hip, call, k, 2, repeats=5)
                 want = oracle.align(batch.emissions, batch.targets, mode=mode, check_inputs=check, threads=16)
                 got = {f: getattr(result, f).cpu().numpy() for f in ("labels", "scores", "status", "objective")}
                 parity = all(np.array_equal(got[f].view(np.int32) if got[f].dtype == np.float32 else got[f],

@@ -162,30 +162,58 @@ std::tuple<std::vector<at::Tensor>, std::vector<int64_t>> run_align(int64_t coun
           std::move(sizes)};
 }
 
-// emission_validity (alignment.cu:893-917).
-at::Tensor emission_validity(at::TensorList emissions) {
-  const int64_t count = emissions.size();
-  TORCH_CHECK(count > 0 && count <= FFA_MAX_BATCH, "provide 1..65535 emission tensors");
-  TORCH_CHECK(emissions[0].is_cuda(), "CUDA emissions required");
-  const auto device = emissions[0].device();
+// The emission scan shared by the operator and the package's Python entry
+// (replaces alignment.cu:893-917 and the Python checks of alignment.py:312-343):
+// every record must be a contiguous fp32 [T, V] tensor on the first record's
+// device with 0 < T <= INT_MAX and 0 < V <= 8192; their {address, numel}
+// descriptors go into a caching-host-allocator block, one asynchronous upload
+// on the current stream, one workgroup per record. `item(i)` returns the i-th
+// tensor or nullptr when the i-th object is not a tensor; `reject(message)`
+// raises the caller's exception type.
+template <class Item, class Reject>
+at::Tensor scan_emissions(int64_t count, Item item, Reject reject, const char* shape_message) {
+  if (count <= 0 || count > FFA_MAX_BATCH) reject("provide 1..65535 emission tensors");
+  const at::Tensor* first = item(0);
+  if (!first || !first->is_cuda()) reject(shape_message);
+  const auto device = first->device();
   c10::hip::HIPGuardMasqueradingAsCUDA guard(device);
   const HIPStreamMasqueradingAsCUDA stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(device.index());
-  auto host = at::empty({count, 2}, at::TensorOptions().dtype(at::kLong).device(at::kCPU).pinned_memory(true));
-  auto* descriptors = host.data_ptr<int64_t>();
+  auto* host_alloc = at::getHostAllocator(at::kCUDA);
+  const int64_t bytes = 16 * count;
+  c10::DataPtr host = host_alloc->allocate(bytes);
+  auto* descriptors = static_cast<int64_t*>(host.get());
+  const void* last = nullptr;
   for (int64_t i = 0; i < count; ++i) {
-    const auto& e = emissions[i];
-    TORCH_CHECK(e.device() == device && e.scalar_type() == at::kFloat && e.dim() == 2 && e.is_contiguous() &&
-                    e.size(0) > 0 && e.size(0) <= INT_MAX && e.size(1) > 0 && e.size(1) <= FFA_MAX_VOCAB,
-                "emissions must be contiguous CUDA FP32 [T,V] on one device with supported dimensions");
-    descriptors[2 * i] = reinterpret_cast<int64_t>(e.data_ptr<float>());
-    descriptors[2 * i + 1] = e.numel();
-    recordStreamMasqueradingAsCUDA(e.storage().data_ptr(), stream);
+    const at::Tensor* e = item(i);
+    if (!e || !(e->is_cuda() && e->device() == device && e->scalar_type() == at::kFloat && e->dim() == 2 &&
+                e->is_contiguous() && e->size(0) > 0 && e->size(0) <= INT_MAX && e->size(1) > 0 &&
+                e->size(1) <= FFA_MAX_VOCAB))
+      reject(shape_message);
+    descriptors[2 * i] = reinterpret_cast<int64_t>(e->data_ptr());
+    descriptors[2 * i + 1] = e->numel();
+    const void* storage = e->storage().data_ptr().get();
+    if (storage != last) recordStreamMasqueradingAsCUDA(e->storage().data_ptr(), stream);
+    last = storage;
   }
-  auto resident = host.to(device, /*non_blocking=*/true);
-  auto result = at::empty({count}, emissions[0].options().dtype(at::kBool));
-  check_ffa(ffa_emission_validity_launch(resident.data_ptr<int64_t>(), count,
-                                         reinterpret_cast<uint8_t*>(result.data_ptr<bool>()), stream.stream()));
+  const auto options = first->options();
+  auto table = at::empty({align256(bytes)}, options.dtype(at::kByte));
+  const hipError_t copied = hipMemcpyAsync(table.data_ptr(), host.get(), bytes, hipMemcpyHostToDevice, stream.stream());
+  TORCH_CHECK(copied == hipSuccess, "fast_forced_aligner: descriptor upload failed: ", hipGetErrorString(copied));
+  host_alloc->record_event(host.get(), host.get_context(), stream.unwrap());
+  auto result = at::empty({count}, options.dtype(at::kBool));
+  check_ffa(ffa_emission_validity_launch(static_cast<const int64_t*>(table.data_ptr()), count,
+                                         reinterpret_cast<uint8_t*>(result.data_ptr()), stream.stream()));
   return result;
+}
+
+// emission_validity operator (the reference schema of alignment.cu:1065):
+// argument errors raise RuntimeError, as the reference operator's checks do.
+at::Tensor emission_validity_op(at::TensorList emissions) {
+  return scan_emissions(
+      (int64_t)emissions.size(),
+      [&](int64_t i) -> const at::Tensor* { return &emissions[i]; },
+      [](const char* message) { TORCH_CHECK(false, message); },
+      "emissions must be contiguous CUDA FP32 [T,V] on one device with supported dimensions");
 }
 
 // align operator (alignment.cu:919-1061): the reference schema and return order.
@@ -299,44 +327,20 @@ py::tuple align_py(py::handle emissions, py::handle targets, py::handle blank_id
   return py::make_tuple(outs, lens);
 }
 
-// Python entry of the package's emission_validity() (alignment.cu:893-917):
-// the same scan as the operator, with the Python layer's per-record checks
-// (alignment.py:312-343) done here in C++ and the descriptors uploaded from a
-// caching-host-allocator block.
+// Python entry of the package's emission_validity(): the operator's scan, with
+// the Python layer's ValueError for malformed arguments (alignment.py:312-343).
 py::object emission_validity_py(py::handle emissions) {
   c10::InferenceMode inference;
   py::object seq = py::reinterpret_steal<py::object>(PySequence_Fast(emissions.ptr(), "emissions"));
   if (!seq) throw py::error_already_set();
-  const int64_t count = PySequence_Fast_GET_SIZE(seq.ptr());
-  if (count <= 0 || count > FFA_MAX_BATCH) throw py::value_error("provide 1..65535 emission tensors");
   PyObject** items = PySequence_Fast_ITEMS(seq.ptr());
-  const char* bad = "emissions must be contiguous CUDA float32 [T,V] with supported dimensions on one device";
-  if (!THPVariable_Check(items[0]) || !THPVariable_Unpack(items[0]).is_cuda()) throw py::value_error(bad);
-  const auto device = THPVariable_Unpack(items[0]).device();
-  c10::hip::HIPGuardMasqueradingAsCUDA guard(device);
-  const HIPStreamMasqueradingAsCUDA stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(device.index());
-  auto* host_alloc = at::getHostAllocator(at::kCUDA);
-  const int64_t bytes = 16 * count;
-  c10::DataPtr host = host_alloc->allocate(bytes);
-  auto* descriptors = static_cast<int64_t*>(host.get());
-  for (int64_t i = 0; i < count; ++i) {
-    if (!THPVariable_Check(items[i])) throw py::value_error(bad);
-    const at::Tensor& e = THPVariable_Unpack(items[i]);
-    if (!(e.is_cuda() && e.device() == device && e.scalar_type() == at::kFloat && e.dim() == 2 && e.is_contiguous() &&
-          e.size(0) > 0 && e.size(0) <= INT_MAX && e.size(1) > 0 && e.size(1) <= FFA_MAX_VOCAB))
-      throw py::value_error(bad);
-    descriptors[2 * i] = reinterpret_cast<int64_t>(e.data_ptr());
-    descriptors[2 * i + 1] = e.numel();
-    recordStreamMasqueradingAsCUDA(e.storage().data_ptr(), stream);
-  }
-  const auto options = THPVariable_Unpack(items[0]).options();
-  auto table = at::empty({align256(bytes)}, options.dtype(at::kByte));
-  const hipError_t copied = hipMemcpyAsync(table.data_ptr(), host.get(), bytes, hipMemcpyHostToDevice, stream.stream());
-  TORCH_CHECK(copied == hipSuccess, "fast_forced_aligner: descriptor upload failed: ", hipGetErrorString(copied));
-  host_alloc->record_event(host.get(), host.get_context(), stream.unwrap());
-  auto result = at::empty({count}, options.dtype(at::kBool));
-  check_ffa(ffa_emission_validity_launch(static_cast<const int64_t*>(table.data_ptr()), count,
-                                         reinterpret_cast<uint8_t*>(result.data_ptr()), stream.stream()));
+  at::Tensor result = scan_emissions(
+      (int64_t)PySequence_Fast_GET_SIZE(seq.ptr()),
+      [&](int64_t i) -> const at::Tensor* {
+        return THPVariable_Check(items[i]) ? &THPVariable_Unpack(items[i]) : nullptr;
+      },
+      [](const char* message) { throw py::value_error(message); },
+      "emissions must be contiguous CUDA float32 [T,V] with supported dimensions on one device");
   return py::reinterpret_steal<py::object>(THPVariable_Wrap(result));
 }
 
@@ -470,7 +474,7 @@ TORCH_LIBRARY(fast_forced_aligner_cuda, m) {
 
 TORCH_LIBRARY_IMPL(fast_forced_aligner_cuda, CUDA, m) {
   m.impl("align", &align_op);
-  m.impl("emission_validity", &emission_validity);
+  m.impl("emission_validity", &emission_validity_op);
 }
 
 PYBIND11_MODULE(_ffa_torch, m) {

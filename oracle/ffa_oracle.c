@@ -28,6 +28,17 @@
 
 #define ORC_EXPORT __attribute__((visibility("default")))
 
+/* Planted-mistake hooks for tests/test_oracle.py: built only into
+ * libffa_oracle_mutants.so (-DORC_MUTANTS), never into libffa_oracle.so.
+ * MUT(n) is true when mistake n is selected; the pins must reject each one. */
+#ifdef ORC_MUTANTS
+static int g_mutant = 0;
+ORC_EXPORT void orc_set_mutant(int n) { g_mutant = n; }
+#define MUT(n) (g_mutant == (n))
+#else
+#define MUT(n) 0
+#endif
+
 typedef struct {
   int64_t chunk_frames;         /* H, py:498 passes 128 */
   int32_t mode;                 /* 0 conventional, 1 chunks without greedy, 2 full (cu:3) */
@@ -102,7 +113,7 @@ static int32_t dp_interval(rec_ctx* c, int64_t a, int64_t b, int resume, int64_t
   float* next = c->next;
   if (!resume) {
     for (int32_t s = 0; s < S; ++s) {
-      prev[s] = (a > 0 || s < 2) ? c->e[a * c->V + c->l[s]] : -INFINITY;
+      prev[s] = ((a > 0 && !MUT(1)) || s < 2) ? c->e[a * c->V + c->l[s]] : -INFINITY;
       c->bp[a * S + s] = 0;
     }
     start_t = a + 1;
@@ -131,7 +142,7 @@ static int32_t dp_interval(rec_ctx* c, int64_t a, int64_t b, int resume, int64_t
     float best = -INFINITY;
     int32_t state = INT32_MAX;
     for (int32_t s = 0; s < S; ++s)
-      if (prev[s] > best || (prev[s] == best && s < state)) { best = prev[s]; state = s; }
+      if (prev[s] > best || (prev[s] == best && (MUT(2) ? s > state : s < state))) { best = prev[s]; state = s; }
     terminal = isnan(prev[0]) ? 0 : state;
   }
   *score = prev[terminal];
@@ -199,7 +210,7 @@ static int greedy_chunk(rec_ctx* c, int64_t a, int64_t b, const uint8_t* alphabe
 static int legal_seam(const rec_ctx* c, int32_t start, int32_t before) { /* cu:157-161 */
   const int32_t jump = start - before;
   return jump == 0 || jump == 1 ||
-         (jump == 2 && c->l[start] != c->blank && c->l[start] != c->l[start - 2]);
+         (jump == 2 && (MUT(9) || (c->l[start] != c->blank && c->l[start] != c->l[start - 2])));
 }
 
 /* One record through the whole pipeline (launch_alignment, cu:669-815, and
@@ -302,12 +313,12 @@ static int orc_record(const float* e, int64_t T, int64_t V, const int64_t* y, in
           if (join) begin = ia[k];
           else {
             if (ib[k] - begin > maximum_proposed) maximum_proposed = ib[k] - begin;
-            if (maximum_proposed > budget) reject = 1;
+            if (MUT(3) ? maximum_proposed > 2 * budget : maximum_proposed > budget) reject = 1;
           }
           before = k;
         }
         if (reject) {
-          d->routing[1] += 1;
+          d->routing[1] = MUT(4) ? 1 : d->routing[1] + 1;
           if (maximum_proposed > d->routing[2]) d->routing[2] = (int32_t)maximum_proposed;
           if (overlap) early = 1;
           run_repairs = 0;
@@ -320,7 +331,7 @@ static int orc_record(const float* e, int64_t T, int64_t V, const int64_t* y, in
           if (ia[k] >= ib[k]) continue;
           iflag[k] = 0;
           const int join = previous < 0 || (isfinite(co[k]) && isfinite(co[previous]) &&
-                                            legal_seam(&c, es[k], ee[previous]));
+                                            legal_seam(&c, es[k], ee[MUT(5) ? group : previous]));
           if (join) group = k;
           else {
             ib[group] = ib[k];
@@ -332,7 +343,7 @@ static int orc_record(const float* e, int64_t T, int64_t V, const int64_t* y, in
         }
         if (merged) {
           d->repair_passes += 1;
-          for (int64_t k = 0; k < n; ++k) if (iflag[k]) d->repaired_frames += ib[k] - ia[k];
+          for (int64_t k = 0; k < n; ++k) if (iflag[k] || MUT(6)) d->repaired_frames += ib[k] - ia[k];
         }
       }
       /* repair DP (cu:727-760); with overlap, a queued record runs the full
@@ -345,6 +356,7 @@ static int orc_record(const float* e, int64_t T, int64_t V, const int64_t* y, in
             resume = 1; start_t = fend[0];
             memcpy(alpha, frontier, sizeof(float) * (size_t)S);
             d->reuse[1] += fend[0]; d->reuse[3] += S;
+            if (MUT(8)) d->reuse[2] += S;
           }
           float score;
           terminal = dp_interval(&c, 0, T, resume, start_t, &score, 0, NULL);
@@ -363,7 +375,7 @@ static int orc_record(const float* e, int64_t T, int64_t V, const int64_t* y, in
             if (saved > a && saved <= b) {
               resume = 1; start_t = saved;
               memcpy(alpha, frontier + (size_t)k * S, sizeof(float) * (size_t)S);
-              d->reuse[0] += saved - a; d->reuse[3] += S;
+              d->reuse[0] += MUT(7) ? saved : saved - a; d->reuse[3] += S;
             }
             d->reuse[2] += S;
           }
@@ -408,6 +420,7 @@ static int orc_record(const float* e, int64_t T, int64_t V, const int64_t* y, in
       resume = 1; start_t = fend[0];
       memcpy(alpha, frontier, sizeof(float) * (size_t)S);
       d->reuse[1] += fend[0]; d->reuse[3] += S;
+      if (MUT(8)) d->reuse[2] += S;
     }
     float score;
     terminal = dp_interval(&c, 0, T, resume, start_t, &score, 0, NULL);

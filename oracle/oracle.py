@@ -42,6 +42,21 @@ def build() -> None:
 
 
 _lib = None
+_mutants = None
+MUTANTS_LIB = HERE / "libffa_oracle_mutants.so"
+
+
+def _declare(handle: ctypes.CDLL) -> ctypes.CDLL:
+    p = ctypes.c_void_p
+    handle.orc_align.restype = ctypes.c_int
+    handle.orc_align.argtypes = [ctypes.c_int64, p, p, p, p, p, p, p, ctypes.POINTER(Options),
+                                 ctypes.c_int32] + [p] * 10 + [p]
+    handle.orc_record_status.restype = ctypes.c_int32
+    handle.orc_record_status.argtypes = [p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                         ctypes.c_int64, ctypes.c_int32, ctypes.c_int32]
+    handle.orc_emission_valid.restype = ctypes.c_int32
+    handle.orc_emission_valid.argtypes = [p, ctypes.c_int64]
+    return handle
 
 
 def lib() -> ctypes.CDLL:
@@ -49,17 +64,22 @@ def lib() -> ctypes.CDLL:
     if _lib is None:
         if not LIB.exists():
             build()
-        _lib = ctypes.CDLL(str(LIB))
-        p = ctypes.c_void_p
-        _lib.orc_align.restype = ctypes.c_int
-        _lib.orc_align.argtypes = [ctypes.c_int64, p, p, p, p, p, p, p, ctypes.POINTER(Options),
-                                   ctypes.c_int32] + [p] * 10 + [p]
-        _lib.orc_record_status.restype = ctypes.c_int32
-        _lib.orc_record_status.argtypes = [p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
-                                           ctypes.c_int64, ctypes.c_int32, ctypes.c_int32]
-        _lib.orc_emission_valid.restype = ctypes.c_int32
-        _lib.orc_emission_valid.argtypes = [p, ctypes.c_int64]
+        _lib = _declare(ctypes.CDLL(str(LIB)))
     return _lib
+
+
+def mutants() -> ctypes.CDLL:
+    """The oracle built with planted-mistake hooks (tests only):
+    ``orc_set_mutant(n)`` selects mistake n (0 = none); pass the handle to
+    ``align(..., library=...)``."""
+    global _mutants
+    if _mutants is None:
+        if not MUTANTS_LIB.exists():
+            build()
+        _mutants = _declare(ctypes.CDLL(str(MUTANTS_LIB)))
+        _mutants.orc_set_mutant.argtypes = [ctypes.c_int]
+        _mutants.orc_set_mutant.restype = None
+    return _mutants
 
 
 def _ptr(a: np.ndarray) -> int:
@@ -77,7 +97,7 @@ def knobs(mode: str) -> Options:
 
 def align(emissions: Sequence[np.ndarray], targets: Sequence[np.ndarray], blank_id=0,
           mode: str = "optimized", check_inputs: bool = True, emission_validity=None,
-          threads: int = 1, options: Options | None = None) -> dict:
+          threads: int = 1, options: Options | None = None, library: ctypes.CDLL | None = None) -> dict:
     """Run the oracle on host arrays; returns a dict of numpy outputs."""
     count = len(emissions)
     blanks = [blank_id] * count if isinstance(blank_id, (int, np.integer)) else list(blank_id)
@@ -107,7 +127,7 @@ def align(emissions: Sequence[np.ndarray], targets: Sequence[np.ndarray], blank_
     if emission_validity is not None:
         validity = np.ascontiguousarray(emission_validity, dtype=np.uint8)
     rows = ctypes.c_int64(0)
-    rc = lib().orc_align(count, _ptr(eptr), _ptr(T), _ptr(V), _ptr(yptr), _ptr(U), _ptr(B),
+    rc = (library or lib()).orc_align(count, _ptr(eptr), _ptr(T), _ptr(V), _ptr(yptr), _ptr(U), _ptr(B),
                          None if validity is None else _ptr(validity), ctypes.byref(o), threads,
                          *[_ptr(out[k]) for k in ("labels", "scores", "status", "objective", "stitched",
                                                   "repair_passes", "repaired_frames", "shortcut_stats",

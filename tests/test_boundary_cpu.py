@@ -107,6 +107,7 @@ def test_plan_sizes_and_gating(lib):
     ([(10, 8, 1, 0)], {"repair_threads": 128}, "overlap preserves fallback geometry"),
     ([(10, 8, 1, 0)], {"trace_min_frames": 0}, "trace_min_frames"),
     ([(10, 8, 1, 0)], {"chunk_frames": 0}, "chunk size or mode"),
+    ([(10, 8, 1, 0)], {"chunk_frames": 513}, "chunk size or mode"),
     ([(10, 8, 1, 0)], {"mode": 3}, "chunk size or mode"),
 ])
 def test_plan_rejects_like_the_reference(lib, shape, changes, message):

@@ -246,3 +246,64 @@ def test_emission_valid():
     assert not O.emission_valid(e)
     e[3, 0] = np.inf
     assert not O.emission_valid(e)
+
+
+# --- optimized-mode repair rounds, budget and frontier: hand-derived pins ---
+
+import repair_cases as RC  # noqa: E402
+
+
+@pytest.mark.parametrize("case", RC.all_cases(), ids=lambda c: c["name"])
+def test_repair_path_hand_derived(case):
+    """Merges, repair passes, repaired frames, frontier resume columns, budget
+    rejection with and without overlap, and the repair_rounds / mode knobs:
+    every output equals the values derived on paper from alignment.cu in
+    tests/repair_cases.py, and the labels equal conventional DP."""
+    knobs = RC.knob_vector(**case["knobs"])
+    out = O.align([case["emissions"]], [case["targets"]], options=RC.oracle_options(knobs))
+    RC.check_expected(out, case)
+    conv = O.align([case["emissions"]], [case["targets"]], mode="conventional")
+    np.testing.assert_array_equal(out["labels"], conv["labels"])
+
+
+# Planted mistakes (oracle/ffa_oracle.c MUT(n), compiled only into the
+# mutants library): each is a plausible misreading of alignment.cu, and each
+# must make at least one hand-derived case fail.
+PLANTED = {
+    1: "strict start at every chunk (no relaxed init for a > 0, cu:409)",
+    2: "chunk terminal takes the highest index on ties (cu:462-492)",
+    3: "budget compared against twice the budget (cu:190-192)",
+    4: "routing_stats[1] set once instead of counted per round (cu:194)",
+    5: "merge pass checks seams against the group's end, not the previous piece's (cu:206-219)",
+    6: "repaired_frames counts every interval, not only merged ones (cu:222-226)",
+    7: "frontier resume counts the saved end, not the resumed frames (cu:378)",
+    8: "the full fallback also counts written frontier values (cu:381)",
+    9: "legal_seam accepts every jump of two (cu:157-161)",
+}
+
+
+@pytest.mark.parametrize("mistake", sorted(PLANTED), ids=lambda n: f"mut{n}")
+def test_repair_pins_reject_planted_mistakes(mistake):
+    lib = O.mutants()
+    failures = 0
+    try:
+        lib.orc_set_mutant(mistake)
+        for case in RC.all_cases():
+            out = O.align([case["emissions"]], [case["targets"]],
+                          options=RC.oracle_options(RC.knob_vector(**case["knobs"])), library=lib)
+            try:
+                RC.check_expected(out, case)
+            except AssertionError:
+                failures += 1
+    finally:
+        lib.orc_set_mutant(0)
+    assert failures > 0, f"no pin rejects: {PLANTED[mistake]}"
+
+
+def test_mutants_library_is_the_oracle_when_no_mistake_is_planted():
+    lib = O.mutants()
+    lib.orc_set_mutant(0)
+    for case in RC.all_cases():
+        out = O.align([case["emissions"]], [case["targets"]],
+                      options=RC.oracle_options(RC.knob_vector(**case["knobs"])), library=lib)
+        RC.check_expected(out, case)
