@@ -33,6 +33,7 @@
 #include <cstdio>
 #include <cstring>
 #include <algorithm>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -2667,6 +2668,65 @@ extern "C" int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_opti
                       : launch_geometry<32, 1, false>(p, NT, lds, optimized, in[I_MAX_FRAMES], stream);
     default: return fail(FFA_E_INVALID, "corrupt plan");
   }
+}
+
+// Allocation-free alignment (ffa_align_launch_noalloc). The descriptor table
+// and the workspace of a call live in this array, one copy per GPU, held until
+// the process ends. In host code `scratch` names a host-side stand-in, not the
+// device memory: the host only ever uses the per-device address that
+// hipGetSymbolAddress returns for it.
+static __device__ __align__(256) unsigned char scratch[FFA_NOALLOC_MAX_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device `device`, looked up
+// once per device (with that device current) and kept.
+int scratch_address(int device, unsigned char** out) {
+  std::lock_guard<std::mutex> lock(g_scratch_lock);
+  if (!g_scratch_ptr[device]) {
+    void* ptr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !ptr)
+      return fail(FFA_E_HIP, std::string("scratch address lookup failed: ") + hipGetErrorString(err));
+    g_scratch_ptr[device] = ptr;
+  }
+  *out = static_cast<unsigned char*>(g_scratch_ptr[device]);
+  return FFA_OK;
+}
+
+}  // namespace
+
+extern "C" int ffa_align_launch_noalloc(const ffa_align_plan* plan, const ffa_align_options* o,
+                                        const void* host_table, const uint8_t* emission_validity,
+                                        const ffa_align_outputs* out, hipStream_t stream) {
+  if (!plan || !o || !host_table || !out) return fail(FFA_E_INVALID, "null plan, options, table or outputs");
+  const int64_t table = align_up(plan->table_bytes, 256);
+  if (plan->table_bytes <= 0 || plan->workspace_bytes <= 0 ||
+      table + plan->workspace_bytes > (int64_t)FFA_NOALLOC_MAX_BYTES)
+    return fail(FFA_E_SIZE, "batch needs " + std::to_string(table + plan->workspace_bytes) +
+                                " bytes of device scratch; the allocation-free entry holds at most " +
+                                std::to_string((int64_t)FFA_NOALLOC_MAX_BYTES) + " (use ffa_align_launch)");
+  int device = -1;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess || device < 0 || device >= kMaxDevices)
+    return fail(FFA_E_HIP, std::string("no usable current device: ") + hipGetErrorString(err));
+  if (stream) {
+    int stream_device = -1;
+    err = hipStreamGetDevice(stream, &stream_device);
+    if (err != hipSuccess) return fail(FFA_E_HIP, std::string("stream query failed: ") + hipGetErrorString(err));
+    if (stream_device != device) return fail(FFA_E_INVALID, "the stream belongs to another device than the current one");
+  }
+  unsigned char* base = nullptr;
+  const int rc = scratch_address(device, &base);
+  if (rc != FFA_OK) return rc;
+  // nothing in the workspace has to start at zero: every kernel writes what it reads
+  err = hipMemcpyAsync(base, host_table, plan->table_bytes, hipMemcpyHostToDevice, stream);
+  if (err != hipSuccess) return fail(FFA_E_HIP, std::string("descriptor upload failed: ") + hipGetErrorString(err));
+  return ffa_align_launch(plan, o, base, emission_validity, out, base + table, stream);
 }
 
 extern "C" int ffa_token_spans_launch(const ffa_span_record* device_records, int64_t count, const int64_t* labels,

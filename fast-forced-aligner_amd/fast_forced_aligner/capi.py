@@ -19,7 +19,7 @@ FFA_MAX_VOCAB = 8192
 FFA_MAX_STATES = 20479
 
 EXPORTED = ("ffa_default_options", "ffa_align_plan_batch", "ffa_align_describe", "ffa_align_launch",
-            "ffa_emission_validity_launch", "ffa_token_spans_launch", "ffa_log_softmax_launch", "ffa_last_error",
+            "ffa_align_launch_noalloc", "ffa_emission_validity_launch", "ffa_token_spans_launch", "ffa_log_softmax_launch", "ffa_last_error",
             "ffa_profile_next_launch", "ffa_launch_floor")
 
 
@@ -73,6 +73,9 @@ def load(path: Path | str = HIP_LIBRARY) -> ctypes.CDLL:
     lib.ffa_align_launch.restype = ctypes.c_int
     lib.ffa_align_launch.argtypes = [ctypes.POINTER(Plan), ctypes.POINTER(Options), p, p,
                                      ctypes.POINTER(Outputs), p, p]
+    lib.ffa_align_launch_noalloc.restype = ctypes.c_int
+    lib.ffa_align_launch_noalloc.argtypes = [ctypes.POINTER(Plan), ctypes.POINTER(Options), p, p,
+                                             ctypes.POINTER(Outputs), p]
     lib.ffa_emission_validity_launch.restype = ctypes.c_int
     lib.ffa_emission_validity_launch.argtypes = [p, ctypes.c_int64, p, p]
     lib.ffa_last_error.restype = ctypes.c_char_p

@@ -125,6 +125,27 @@ int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_options* option
                      const void* device_table, const uint8_t* emission_validity,
                      const ffa_align_outputs* outputs, void* workspace, hipStream_t stream);
 
+/* Allocation-free variant of ffa_align_launch. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The descriptor table and the workspace live in a device array of
+ * FFA_NOALLOC_MAX_BYTES that the library holds on each GPU it runs on until the
+ * process ends; host_table (the bytes ffa_align_describe wrote, best in pinned
+ * memory, kept unchanged until the stream reaches the work) is copied into it
+ * on `stream`. The caller passes inputs and outputs as for ffa_align_launch;
+ * `stream` must belong to the current device. Nothing is allocated or freed.
+ * Returns FFA_E_SIZE when the plan's table (rounded up to 256 bytes) plus its
+ * workspace exceed FFA_NOALLOC_MAX_BYTES (32 MiB: about 12 MiB serves 64
+ * records of 250..1,750 frames and ~500 tokens; four 30,000-frame records of
+ * 9,000 tokens need 580 MiB and must use ffa_align_launch).
+ * Every call on a GPU shares that GPU's array: calls enqueued on one stream
+ * are ordered, but calls that overlap on one GPU (several streams or threads)
+ * race and corrupt each other's results. */
+#define FFA_NOALLOC_MAX_BYTES (32u << 20)
+int ffa_align_launch_noalloc(const ffa_align_plan* plan, const ffa_align_options* options, const void* host_table,
+                             const uint8_t* emission_validity, const ffa_align_outputs* outputs,
+                             hipStream_t stream);
+
 /* Replaces emission_validity (alignment.cu:893-917 and its kernel :879-891).
  * device_descriptors: [count][2] int64 {device address of a float array, element
  * count}, the reference's descriptor layout. valid: device bool[count]. */

@@ -1,0 +1,99 @@
+"""The allocation-free entry point (ffa_align_launch_noalloc): its outputs
+equal ffa_align_launch's bit for bit, on two calls in a row whose second batch
+is smaller (the shared device array keeps the first call's contents), and a
+batch beyond its fixed scratch is refused."""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from fast_forced_aligner import capi, workloads
+from helpers import FIELDS, assert_same
+
+DEV = "cuda"
+
+
+def _records(es, ys):
+    recs = (capi.Record * len(es))()
+    for i, (e, y) in enumerate(zip(es, ys)):
+        recs[i] = capi.Record(e.data_ptr(), y.data_ptr() if y.numel() else None, e.shape[0], e.shape[1],
+                              y.numel(), 0)
+    return recs
+
+
+def _outputs(plan, count):
+    N = plan.total_frames
+    outs = {"labels": torch.full((N,), -7, dtype=torch.int64, device=DEV),
+            "scores": torch.full((N,), 7.0, dtype=torch.float32, device=DEV),
+            "status": torch.full((count,), 7, dtype=torch.int32, device=DEV),
+            "objective": torch.full((count,), 7.0, dtype=torch.float32, device=DEV),
+            "stitched": torch.full((count,), 7, dtype=torch.int32, device=DEV),
+            "repair_passes": torch.full((count,), 7, dtype=torch.int32, device=DEV),
+            "repaired_frames": torch.full((count,), 7, dtype=torch.int64, device=DEV),
+            "shortcut_stats": torch.full((count, 3), 7, dtype=torch.int64, device=DEV),
+            "routing_stats": torch.full((count, 3), 7, dtype=torch.int32, device=DEV),
+            "reuse_stats": torch.full((plan.reuse_rows, 4), 7, dtype=torch.int64, device=DEV)}
+    ptrs = capi.Outputs(*[outs[f].data_ptr() if outs[f].numel() else None for f in FIELDS])
+    return outs, ptrs
+
+
+def _run(lib, es, ys, optimized, noalloc):
+    recs = _records(es, ys)
+    o = capi.default_options(lib, optimized)
+    plan = capi.Plan()
+    capi.check(lib, lib.ffa_align_plan_batch(recs, len(es), ctypes.byref(o), ctypes.byref(plan)))
+    host = torch.empty(plan.table_bytes, dtype=torch.uint8).pin_memory()
+    capi.check(lib, lib.ffa_align_describe(ctypes.byref(plan), recs, host.data_ptr(), plan.table_bytes))
+    outs, ptrs = _outputs(plan, len(es))
+    stream = torch.cuda.current_stream().cuda_stream
+    if noalloc:
+        capi.check(lib, lib.ffa_align_launch_noalloc(ctypes.byref(plan), ctypes.byref(o), host.data_ptr(), None,
+                                                     ctypes.byref(ptrs), stream))
+    else:
+        table = host.to(DEV)
+        ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=DEV)
+        capi.check(lib, lib.ffa_align_launch(ctypes.byref(plan), ctypes.byref(o), table.data_ptr(), None,
+                                             ctypes.byref(ptrs), ws.data_ptr(), stream))
+    torch.cuda.synchronize()
+    return {f: outs[f].cpu().numpy() for f in FIELDS}
+
+
+def _device(batch):
+    return ([torch.from_numpy(e).to(DEV) for e in batch.emissions],
+            [torch.from_numpy(y).to(DEV) for y in batch.targets])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("optimized", [True, False], ids=["optimized", "conventional"])
+def test_noalloc_matches_launch_on_two_calls(optimized):
+    lib = capi.load()
+    big = _device(workloads.make("c5"))        # 1,024 records: ~11 MiB of scratch
+    small = _device(workloads.c2(batch=12))    # then a smaller batch over the stale contents
+    for name, (es, ys) in (("c5", big), ("c2x12", small)):
+        print(f"noalloc {name} optimized={optimized}", flush=True)
+        want = _run(lib, es, ys, optimized, noalloc=False)
+        got = _run(lib, es, ys, optimized, noalloc=True)
+        assert_same(got, want, where=f"noalloc {name} ")
+        assert not (got["labels"] == -7).all()
+
+
+def test_noalloc_rejects_batches_beyond_its_scratch():
+    """Host-side size check before any device work: four 30,000-frame records of
+    9,000 tokens need ~580 MiB of workspace. No GPU needed (fake addresses are
+    never dereferenced)."""
+    lib = capi.load()
+    recs = (capi.Record * 4)()
+    for i in range(4):
+        recs[i] = capi.Record(0x1000 * (i + 1), 0x9000 * (i + 1), 30000, 32, 9000, 0)
+    o = capi.default_options(lib, True)
+    plan = capi.Plan()
+    capi.check(lib, lib.ffa_align_plan_batch(recs, 4, ctypes.byref(o), ctypes.byref(plan)))
+    host = (ctypes.c_uint8 * plan.table_bytes)()
+    capi.check(lib, lib.ffa_align_describe(ctypes.byref(plan), recs, host, plan.table_bytes))
+    outs = capi.Outputs(*([0x1000] * 10))
+    assert lib.ffa_align_launch_noalloc(ctypes.byref(plan), ctypes.byref(o), host, None, ctypes.byref(outs),
+                                        None) == -3
+    assert "at most 33554432" in lib.ffa_last_error().decode()
