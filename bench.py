@@ -46,6 +46,29 @@ def hip_runtime():
     return lib
 
 
+_SLEEP_CYCLES_PER_US = None
+
+
+def hold_stream(us):
+    """Keeps the current stream busy for about `us` microseconds with torch's
+    bounded spin kernel, so that the launches enqueued behind it are all in
+    the queue before the GPU reaches them. Event pairs around a kernel then
+    time the kernel itself, not how long the host took to submit it (without
+    this, a GPU that outruns the host starts the timing event early)."""
+    import torch
+
+    global _SLEEP_CYCLES_PER_US
+    if _SLEEP_CYCLES_PER_US is None:
+        torch.cuda._sleep(100000)  # warm the spin kernel
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        torch.cuda._sleep(1000000)
+        b.record()
+        b.synchronize()
+        _SLEEP_CYCLES_PER_US = 1000000 / max(a.elapsed_time(b) * 1e3, 1.0)
+    torch.cuda._sleep(int(us * _SLEEP_CYCLES_PER_US))
+
+
 def measure(capi_lib, hip, call, steps, warmup, repeats=5):
     """Pipelined wall time per call of `call` (an align entry): `repeats`
     passes of `steps` calls back to back with nothing else on the host between
@@ -53,7 +76,9 @@ def measure(capi_lib, hip, call, steps, warmup, repeats=5):
     the average duration of its dominant kernel, from timing-only HIP events
     armed around that kernel in `repeats` further passes of `steps` calls (the
     event records are host work of their own, so they stay out of the
-    throughput passes); the median pass."""
+    throughput passes; the stream is held while they are enqueued, so that
+    each event pair times its kernel rather than the host's submission); the
+    median pass."""
     import statistics
 
     import torch
@@ -80,6 +105,7 @@ def measure(capi_lib, hip, call, steps, warmup, repeats=5):
             starts.append(a)
             stops.append(b)
         torch.cuda.synchronize()
+        hold_stream(steps * 60.0)
         for i in range(steps):
             capi_lib.ffa_profile_next_launch(starts[i], stops[i])
             result = call()
@@ -97,7 +123,8 @@ def measure(capi_lib, hip, call, steps, warmup, repeats=5):
 
 def launch_floor(capi_lib, hip, workgroups, steps):
     """Mean duration, timed like the dominant kernel (one timing-only event
-    pair per launch, launches back to back on the current stream), of a kernel
+    pair per launch, launches back to back on the current stream behind a
+    held stream), of a kernel
     that does nothing, launched with the dominant kernel's workgroup count: the
     fixed cost of one dispatch under this timing method, beneath every
     measured kernel duration (the block size does not change it)."""
@@ -113,6 +140,7 @@ def launch_floor(capi_lib, hip, workgroups, steps):
     for _ in range(10):
         assert capi_lib.ffa_launch_floor(workgroups, 256, stream) == 0
     torch.cuda.synchronize()
+    hold_stream(steps * 20.0)
     for a, b in pairs:
         assert hip.hipEventRecord(a, stream) == 0
         assert capi_lib.ffa_launch_floor(workgroups, 256, stream) == 0

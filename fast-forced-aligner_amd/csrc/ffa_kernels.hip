@@ -35,6 +35,7 @@
 #include <algorithm>
 #include <mutex>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "ffa.h"
@@ -49,16 +50,35 @@ constexpr int TAIL_SLOT_CAP = 512;  // record tails with more chunks plan in glo
 constexpr int YTOK_PAD = 72;        // sentinel entries after the staged targets
 constexpr int EBLK_COLS = 64;       // widest row (V) staged in LDS blocks by the DP
 
-struct RecordDesc {  // device descriptor table entry, 64 bytes
+// Record descriptor, 64 bytes. The first 32 bytes hold what a chunk
+// workgroup needs to find its record and to request its rows and targets.
+struct RecordDesc {
   const float* emissions;
   const int64_t* targets;
-  int64_t frames;
+  int32_t frames;           // T <= INT32_MAX
+  int32_t chunk_offset;     // first chunk of the record in the batch's chunk order
+  int32_t vocab, tokens;
   int64_t frame_offset;     // into labels / scores
   int64_t bp_offset;        // 32-bit words into the backpointer scratch
   int64_t frontier_offset;  // floats into the frontier scratch; -1 when unused
-  int32_t vocab, tokens, blank, chunk_offset;
+  int32_t blank, pad;
 };
 static_assert(sizeof(RecordDesc) == 64, "descriptor layout");
+
+// The record table passed by value as a kernel argument (batches of at most
+// FFA_TABLE_ARG_RECORDS records): the runtime copies it with the launch, so
+// no upload, no copy kernel and no host synchronization object is needed, and
+// a chunk workgroup finds its record in one round of loads. Larger batches
+// upload the table into the workspace instead (NoTable kernels).
+constexpr int ARG_RECORDS = FFA_TABLE_ARG_RECORDS;
+struct alignas(16) ArgTable {
+  RecordDesc rec[ARG_RECORDS];
+};
+struct NoTable {
+  int32_t unused;
+};
+template <class TB>
+constexpr bool kArgs = sizeof(TB) == sizeof(ArgTable);
 
 struct Slot {  // per-chunk state of optimized mode (cu:1021-1029 buffers), 32 bytes
   int32_t a, b, start, end, frontier_end;
@@ -1718,12 +1738,14 @@ __device__ __attribute__((always_inline)) int greedy_fast(const Lds& L, const fl
 // ---------------------------------------------------------------------------
 // Kernels.
 
-template <int K, int D, bool LG>
-__global__ void __launch_bounds__(K == 32 ? 640 : 256) conventional_kernel(Params p) {
+template <int K, int D, bool LG, class TB>
+__global__ void __launch_bounds__(K == 32 ? 640 : 256) conventional_kernel(Params p, TB tab) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   const Lds L = carve(lds_raw, p);
   const int rec = blockIdx.x;
-  const RecordDesc d = load_pod(glb(p.desc) + rec);
+  RecordDesc d;
+  if constexpr (kArgs<TB>) d = tab.rec[rec];
+  else d = load_pod(glb(p.desc) + rec);
   Rec r = make_rec(d, p, L);
   if (LG) r.st = p.stats + d.frame_offset;
   const Staged st = stage_tokens<ALPHABET_NONE>(d, p, rec, L);
@@ -1999,49 +2021,93 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
 // stages and validates the record's targets, takes the greedy shortcut
 // (cu:30-153) or runs the relaxed chunk DP (cu:721-726), and writes the
 // chunk's labels, scores and slot.
-template <int K, int D, bool LG>
-__global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p) {
+template <int K, int D, bool LG, class TB>
+__global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p, TB tab) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   const Lds L = carve(lds_raw, p);
   const int tid = threadIdx.x;
   const int slot_index = xcd_slot(blockIdx.x, p.total_slots);
   if (slot_index >= p.total_slots) return;
-  const ChunkEntry ce = load_uniform(p.chunks + slot_index);
-  const int rec = (int)(ce.hi & 0xffffu);
-  const int n = (int)((ce.hi >> 16) & 0x1ffu) + 1;
-  const int64_t chunk = (int64_t)(ce.hi >> 25);
-  const bool fast = ((ce.lo >> ENTRY_FAST_SHIFT) & 1u) != 0;
-  const int quads = (int)((ce.lo >> ENTRY_QUADS_SHIFT) & 7u) + 1;  // V / 4 (fast path)
-  const int U = (int)((ce.lo >> ENTRY_U_SHIFT) & 0x3fffu);
-  const GLB int64_t* y = (const GLB int64_t*)((ce.lo & ((1ull << ENTRY_U_SHIFT) - 1)) << 3);
+  int rec, n, U;
+  int64_t chunk;
+  bool fast;
+  int quads;  // V / 4 (fast path)
+  const GLB int64_t* y;
+  RecordDesc d;
+  TargetLoads tl;
+  if constexpr (kArgs<TB>) {
+    // Table in the kernel arguments: lane i of every wave reads the first 32
+    // bytes of record i's descriptor (the batch has at most 64 records); the
+    // record is the last one whose first chunk is at or before this one.
+    const int lane = tid & 63;
+    const bool mine = lane < p.count;
+    const RecordDesc& lr = tab.rec[mine ? lane : 0];
+    const v4i_t h0 = *reinterpret_cast<const v4i_t*>(&lr.emissions);
+    const v4i_t h1 = *reinterpret_cast<const v4i_t*>(&lr.frames);
+    const uint64_t below = __ballot(mine && h1[1] <= slot_index);
+    rec = 63 - (int)__builtin_clzll(below);
+    const int e_lo = __builtin_amdgcn_readlane(h0[0], rec), e_hi = __builtin_amdgcn_readlane(h0[1], rec);
+    const int y_lo = __builtin_amdgcn_readlane(h0[2], rec), y_hi = __builtin_amdgcn_readlane(h0[3], rec);
+    d.emissions = reinterpret_cast<const float*>((uint64_t)(uint32_t)e_lo | (uint64_t)(uint32_t)e_hi << 32);
+    d.targets = reinterpret_cast<const int64_t*>((uint64_t)(uint32_t)y_lo | (uint64_t)(uint32_t)y_hi << 32);
+    d.frames = __builtin_amdgcn_readlane(h1[0], rec);
+    d.chunk_offset = __builtin_amdgcn_readlane(h1[1], rec);
+    d.vocab = __builtin_amdgcn_readlane(h1[2], rec);
+    d.tokens = __builtin_amdgcn_readlane(h1[3], rec);
+    chunk = slot_index - d.chunk_offset;
+    n = (int)min((int64_t)p.H, (int64_t)d.frames - chunk * p.H);
+    U = d.tokens;
+    y = glb(d.targets);
+    fast = p.mode == 2 && p.H <= 128 && d.vocab <= 32 && (d.vocab & 3) == 0 &&
+           (reinterpret_cast<uintptr_t>(d.emissions) & 15) == 0;
+    quads = d.vocab >> 2;
+    tl = issue_targets(y, U, p);
+    const RecordDesc& rd = tab.rec[rec];  // the other half: uniform loads
+    d.frame_offset = rd.frame_offset;
+    d.bp_offset = rd.bp_offset;
+    d.frontier_offset = rd.frontier_offset;
+    d.blank = rd.blank;
+    d.pad = 0;
+  } else {
+    const ChunkEntry ce = load_uniform(p.chunks + slot_index);
+    rec = (int)(ce.hi & 0xffffu);
+    n = (int)((ce.hi >> 16) & 0x1ffu) + 1;
+    chunk = (int64_t)(ce.hi >> 25);
+    fast = ((ce.lo >> ENTRY_FAST_SHIFT) & 1u) != 0;
+    quads = (int)((ce.lo >> ENTRY_QUADS_SHIFT) & 7u) + 1;
+    U = (int)((ce.lo >> ENTRY_U_SHIFT) & 0x3fffu);
+    y = (const GLB int64_t*)((ce.lo & ((1ull << ENTRY_U_SHIFT) - 1)) << 3);
+    // The record descriptor and the first batch of targets are requested
+    // together (the entry holds the targets' address and count).
+    const Pending<RecordDesc> pd = issue_uniform(p.desc + rec);
+    tl = issue_targets(y, U, p);
+    d = finish_uniform(pd);
+  }
   const int64_t a = chunk * p.H;
   const int64_t b = a + n;
-  // The record descriptor and the first batch of targets are requested
-  // together (the entry holds the targets' address and count); the chunk's
-  // rows follow as soon as the descriptor is in (fast path: lane f of waves
-  // 0-1 loads row a+f).
-  const Pending<RecordDesc> pd = issue_uniform(p.desc + rec);
-  TargetLoads tl = issue_targets(y, U, p);
-  const RecordDesc d = finish_uniform(pd);
-  // Every thread issues the same eight 16-byte loads: the row's quads (the
-  // chunk's last row for lanes past it), then -inf for quads past V (chunks
-  // off the fast path read their record's 64-byte descriptor instead; values
-  // unused). With a fixed count the compiler's waits for the targets in the
-  // staging below count these loads exactly instead of waiting for them.
-  // Lanes past the chunk's rows hit lines already requested by lane n-1: no
-  // extra HBM traffic.
+  // The chunk's rows (fast path: lane f of waves 0-1 loads row a+f). Every
+  // thread issues the same eight 16-byte loads: the row's quads (the chunk's
+  // last row for lanes past it), then -inf for quads past V (chunks off the
+  // fast path read the 64-byte -inf constant block instead; values unused).
+  // With a fixed count the compiler's waits for the targets in the staging
+  // below count these loads exactly instead of waiting for them. Lanes past
+  // the chunk's rows hit lines already requested by lane n-1: no extra HBM
+  // traffic.
   float x[32];
   {
-    const GLB v4f_t* src = fast ? (const GLB v4f_t*)glb(d.emissions + (a + min(tid, n - 1)) * (int64_t)d.vocab)
-                                : (const GLB v4f_t*)glb(p.desc + rec);
     const GLB v4f_t* pad = (const GLB v4f_t*)glb(kNegInfQuad);
-    const int qmax = fast ? quads - 1 : 3;
+    const GLB v4f_t* src = fast ? (const GLB v4f_t*)glb(d.emissions + (a + min(tid, n - 1)) * (int64_t)d.vocab) : pad;
+    const int qmax = fast ? quads - 1 : 0;
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-      const v4f_t v = *(q <= qmax ? src + q : pad);
+      const v4f_t v = *(q <= qmax ? src + (fast ? q : 0) : pad);
       x[4 * q] = v.x; x[4 * q + 1] = v.y; x[4 * q + 2] = v.z; x[4 * q + 3] = v.w;
     }
   }
+  // the tail kernel reads the record's descriptor from the workspace (stored
+  // after the row loads are issued, so the waits for the targets do not count it)
+  if constexpr (kArgs<TB>)
+    if (chunk == 0 && tid == 0) store_pod(glb(const_cast<RecordDesc*>(p.desc)) + rec, d);
   const Staged st = fast ? finish_targets<ALPHABET_MASK32, true, true>(tl, d.vocab, d.blank, d.frames, rec, p, L)
                    : p.mode == 2 ? finish_targets<ALPHABET_BITMAP, false, true>(tl, d.vocab, d.blank, d.frames, rec, p, L)
                                  : finish_targets<ALPHABET_NONE, false, true>(tl, d.vocab, d.blank, d.frames, rec, p, L);
@@ -2273,8 +2339,11 @@ __global__ void __launch_bounds__(256) spans_kernel(const ffa_span_record* recs,
 // Conventional mode with logits input: the row statistics of every frame,
 // one workgroup per 128 frames of a record (grid: frame groups x records),
 // before the full-record DP reads them.
-__global__ void __launch_bounds__(256) stats_kernel(Params p) {
-  const RecordDesc d = load_uniform(p.desc + blockIdx.y);
+template <class TB>
+__global__ void __launch_bounds__(256) stats_kernel(Params p, TB tab) {
+  RecordDesc d;
+  if constexpr (kArgs<TB>) d = tab.rec[blockIdx.y];
+  else d = load_uniform(p.desc + blockIdx.y);
   const int64_t a = (int64_t)blockIdx.x * 128;
   if (a >= d.frames) return;
   const int n = (int)min((int64_t)128, d.frames - a);
@@ -2356,22 +2425,23 @@ inline int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 enum {
   I_K, I_NT, I_SLOTS, I_LDS, I_UCAP, I_DCAP, I_VWORDS, I_TAILSLOTS, I_FRONTIER, I_BUDGET,
   I_OVERLAP, I_WS_SLOTS, I_WS_FRONTIER, I_MODE, I_H, I_FMIN, I_REPAIR_MIN, I_EBLK, I_LOGITS, I_WS_STATS,
-  I_MAX_FRAMES
+  I_MAX_FRAMES, I_WS_BP
 };
 
-template <int K, int D, bool LG>
-int launch_geometry(const ffa::Params& p, int NT, size_t lds, bool optimized, int64_t max_frames, hipStream_t stream) {
+template <int K, int D, bool LG, class TB>
+int launch_geometry(const ffa::Params& p, const TB& tab, int NT, size_t lds, bool optimized, int64_t max_frames,
+                    hipStream_t stream) {
   hipEvent_t start = g_profile_start, stop = g_profile_stop;
   g_profile_start = g_profile_stop = nullptr;
   if (p.logits && !optimized)
-    hipLaunchKernelGGL(ffa::stats_kernel, dim3((unsigned)((max_frames + 127) / 128), (unsigned)p.count), dim3(256), 0,
-                       stream, p);
+    hipLaunchKernelGGL(ffa::stats_kernel<TB>, dim3((unsigned)((max_frames + 127) / 128), (unsigned)p.count), dim3(256),
+                       0, stream, p, tab);
   if (start) (void)hipEventRecord(start, stream);
   if (!optimized) {
-    hipLaunchKernelGGL((ffa::conventional_kernel<K, D, LG>), dim3(p.count), dim3(NT), lds, stream, p);
+    hipLaunchKernelGGL((ffa::conventional_kernel<K, D, LG, TB>), dim3(p.count), dim3(NT), lds, stream, p, tab);
   } else {
     const int grid = 8 * ((p.total_slots + 7) / 8);
-    hipLaunchKernelGGL((ffa::chunk_kernel<K, D, LG>), dim3(grid), dim3(std::max(NT, 128)), lds, stream, p);
+    hipLaunchKernelGGL((ffa::chunk_kernel<K, D, LG, TB>), dim3(grid), dim3(std::max(NT, 128)), lds, stream, p, tab);
   }
   if (stop) (void)hipEventRecord(stop, stream);
   if (optimized) hipLaunchKernelGGL((ffa::tail_kernel<K, D, LG>), dim3(p.count), dim3(NT), lds, stream, p);
@@ -2515,7 +2585,15 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
     for (int64_t f = 32; f >= 16 && !eblk_frames; f /= 2)
       if (lds + 8 * f * ffa::EBLK_COLS <= 64 * 1024) eblk_frames = f;
   lds += 8 * eblk_frames * ffa::EBLK_COLS;
-  int64_t ws = align_up(4 * bp_words, 256);
+  // workspace: the record table (uploaded batches: the whole table; batches
+  // passed in the kernel arguments: the descriptors the chunk kernel copies
+  // for the tail kernel), backpointers, chunk slots, frontiers, statistics
+  const bool uploaded = count > ffa::ARG_RECORDS;
+  const int64_t table_bytes =
+      count * (int64_t)sizeof(ffa::RecordDesc) + (uploaded ? (int64_t)sizeof(ffa::ChunkEntry) * slots : 0);
+  int64_t ws = align_up(table_bytes, 256);
+  const int64_t ws_bp = ws;
+  ws += align_up(4 * bp_words, 256);
   const int64_t ws_slots = ws;
   ws += align_up(32 * slots, 256);
   const int64_t ws_frontier = ws;
@@ -2525,7 +2603,8 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
   std::memset(plan, 0, sizeof(*plan));
   plan->count = count;
   plan->total_frames = total_frames;
-  plan->table_bytes = count * (int64_t)sizeof(ffa::RecordDesc) + (int64_t)sizeof(ffa::ChunkEntry) * slots;
+  plan->table_bytes = table_bytes;
+  plan->table_uploaded = uploaded ? 1 : 0;
   plan->workspace_bytes = std::max<int64_t>(ws, 256);
   plan->reuse_rows = frontier ? count : 0;
   int64_t* in = plan->internal;
@@ -2550,6 +2629,7 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
   in[I_LOGITS] = logits ? 1 : 0;
   in[I_WS_STATS] = ws_stats;
   in[I_MAX_FRAMES] = max_frames;
+  in[I_WS_BP] = ws_bp;
   return FFA_OK;
 }
 
@@ -2571,20 +2651,21 @@ int ffa_align_describe(const ffa_align_plan* plan, const ffa_record* records, vo
     ffa::RecordDesc& d = desc[i];
     d.emissions = r.emissions;
     d.targets = r.targets;
-    d.frames = r.frames;
-    d.frame_offset = frame;
-    d.bp_offset = bp;
+    d.frames = (int32_t)r.frames;
+    d.chunk_offset = slot;
     d.vocab = (int32_t)r.vocab;
     d.tokens = (int32_t)r.tokens;
-    d.blank = (int32_t)r.blank;
-    d.chunk_offset = slot;
+    d.frame_offset = frame;
+    d.bp_offset = bp;
     d.frontier_offset = -1;
+    d.blank = (int32_t)r.blank;
+    d.pad = 0;
     const int64_t n = 1 + (r.frames - 1) / H;
     if (frontier && r.frames >= in[I_FMIN]) {  // alignment.cu:374: per-record frontier storage
       d.frontier_offset = fr;
       fr += n * S;
     }
-    if (optimized) {
+    if (optimized && plan->table_uploaded) {
       // greedy fast path: whole rows in registers (V <= 32, 16-byte rows) and
       // one frame per lane of two waves
       const bool fast = in[I_MODE] == 2 && H <= 128 && r.vocab <= 32 && r.vocab % 4 == 0 &&
@@ -2598,8 +2679,8 @@ int ffa_align_describe(const ffa_align_plan* plan, const ffa_record* records, vo
         e.lo = lo;
         e.hi = (uint64_t)i | (uint64_t)(std::min<int64_t>(H, r.frames - c * H) - 1) << 16 | (uint64_t)c << 25;
       }
-      slot += (int32_t)n;
     }
+    if (optimized) slot += (int32_t)n;
     frame += r.frames;
     bp += r.frames * stride_of(S);
   }
@@ -2608,19 +2689,22 @@ int ffa_align_describe(const ffa_align_plan* plan, const ffa_record* records, vo
 
 }  // extern "C"
 
-extern "C" int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_options* o, const void* device_table,
+extern "C" int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_options* o, const void* host_table,
                                 const uint8_t* emission_validity, const ffa_align_outputs* out, void* workspace,
                                 hipStream_t stream) {
   const int64_t* in = plan->internal;
   const bool optimized = in[I_MODE] != 0;
-  if (!device_table || !workspace || !out->labels || !out->scores || !out->status || !out->objective ||
+  if (!host_table || !workspace || !out->labels || !out->scores || !out->status || !out->objective ||
       !out->stitched || !out->repair_passes || !out->repaired_frames || !out->shortcut_stats || !out->routing_stats)
     return fail(FFA_E_INVALID, "null table, workspace or output pointer");
   if (plan->reuse_rows > 0 && !out->reuse_stats) return fail(FFA_E_INVALID, "reuse_stats required for this plan");
   if (o->mode != in[I_MODE] || o->chunk_frames != in[I_H] || (o->logits != 0) != (in[I_LOGITS] != 0))
     return fail(FFA_E_INVALID, "options differ from the plan");
+  auto* ws = static_cast<unsigned char*>(workspace);
   ffa::Params p{};
-  p.desc = static_cast<const ffa::RecordDesc*>(device_table);
+  // the record table: in the workspace's head (uploaded batches), or the
+  // descriptor copies the chunk kernel leaves there for the tail kernel
+  p.desc = reinterpret_cast<const ffa::RecordDesc*>(ws);
   p.chunks = reinterpret_cast<const ffa::ChunkEntry*>(p.desc + plan->count);
   p.validity = emission_validity;
   p.labels = out->labels;
@@ -2633,8 +2717,7 @@ extern "C" int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_opti
   p.shortcut_stats = out->shortcut_stats;
   p.routing_stats = out->routing_stats;
   p.reuse_stats = plan->reuse_rows > 0 ? out->reuse_stats : nullptr;
-  auto* ws = static_cast<unsigned char*>(workspace);
-  p.bp = reinterpret_cast<uint32_t*>(ws);
+  p.bp = reinterpret_cast<uint32_t*>(ws + in[I_WS_BP]);
   p.slots = reinterpret_cast<ffa::Slot*>(ws + in[I_WS_SLOTS]);
   p.frontiers = reinterpret_cast<float*>(ws + in[I_WS_FRONTIER]);
   p.budget = in[I_BUDGET];
@@ -2657,17 +2740,32 @@ extern "C" int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_opti
   p.stats = p.logits ? reinterpret_cast<float2*>(ws + in[I_WS_STATS]) : nullptr;
   const int NT = (int)in[I_NT];
   const size_t lds = (size_t)in[I_LDS];
-  switch (in[I_K]) {
-    case 4: return p.logits ? launch_geometry<4, 8, true>(p, NT, lds, optimized, in[I_MAX_FRAMES], stream)
-                      : launch_geometry<4, 8, false>(p, NT, lds, optimized, in[I_MAX_FRAMES], stream);
-    case 8: return p.logits ? launch_geometry<8, 6, true>(p, NT, lds, optimized, in[I_MAX_FRAMES], stream)
-                      : launch_geometry<8, 6, false>(p, NT, lds, optimized, in[I_MAX_FRAMES], stream);
-    case 16: return p.logits ? launch_geometry<16, 4, true>(p, NT, lds, optimized, in[I_MAX_FRAMES], stream)
-                      : launch_geometry<16, 4, false>(p, NT, lds, optimized, in[I_MAX_FRAMES], stream);
-    case 32: return p.logits ? launch_geometry<32, 1, true>(p, NT, lds, optimized, in[I_MAX_FRAMES], stream)
-                      : launch_geometry<32, 1, false>(p, NT, lds, optimized, in[I_MAX_FRAMES], stream);
-    default: return fail(FFA_E_INVALID, "corrupt plan");
+  const int64_t max_frames = in[I_MAX_FRAMES];
+  auto run = [&](const auto& tab) -> int {
+    using TB = std::decay_t<decltype(tab)>;
+    switch (in[I_K]) {
+      case 4: return p.logits ? launch_geometry<4, 8, true, TB>(p, tab, NT, lds, optimized, max_frames, stream)
+                              : launch_geometry<4, 8, false, TB>(p, tab, NT, lds, optimized, max_frames, stream);
+      case 8: return p.logits ? launch_geometry<8, 6, true, TB>(p, tab, NT, lds, optimized, max_frames, stream)
+                              : launch_geometry<8, 6, false, TB>(p, tab, NT, lds, optimized, max_frames, stream);
+      case 16: return p.logits ? launch_geometry<16, 4, true, TB>(p, tab, NT, lds, optimized, max_frames, stream)
+                               : launch_geometry<16, 4, false, TB>(p, tab, NT, lds, optimized, max_frames, stream);
+      case 32: return p.logits ? launch_geometry<32, 1, true, TB>(p, tab, NT, lds, optimized, max_frames, stream)
+                               : launch_geometry<32, 1, false, TB>(p, tab, NT, lds, optimized, max_frames, stream);
+      default: return fail(FFA_E_INVALID, "corrupt plan");
+    }
+  };
+  if (plan->table_uploaded) {
+    const hipError_t err = hipMemcpyAsync(ws, host_table, plan->table_bytes, hipMemcpyHostToDevice, stream);
+    if (err != hipSuccess) return fail(FFA_E_HIP, std::string("descriptor upload failed: ") + hipGetErrorString(err));
+    return run(ffa::NoTable{0});
   }
+  if (plan->count > ffa::ARG_RECORDS || plan->table_bytes != plan->count * (int64_t)sizeof(ffa::RecordDesc))
+    return fail(FFA_E_INVALID, "corrupt plan");
+  ffa::ArgTable tab;
+  std::memcpy(tab.rec, host_table, plan->table_bytes);
+  std::memset(tab.rec + plan->count, 0, sizeof(tab) - plan->table_bytes);
+  return run(tab);
 }
 
 // Allocation-free alignment (ffa_align_launch_noalloc). The descriptor table
@@ -2704,10 +2802,8 @@ extern "C" int ffa_align_launch_noalloc(const ffa_align_plan* plan, const ffa_al
                                         const void* host_table, const uint8_t* emission_validity,
                                         const ffa_align_outputs* out, hipStream_t stream) {
   if (!plan || !o || !host_table || !out) return fail(FFA_E_INVALID, "null plan, options, table or outputs");
-  const int64_t table = align_up(plan->table_bytes, 256);
-  if (plan->table_bytes <= 0 || plan->workspace_bytes <= 0 ||
-      table + plan->workspace_bytes > (int64_t)FFA_NOALLOC_MAX_BYTES)
-    return fail(FFA_E_SIZE, "batch needs " + std::to_string(table + plan->workspace_bytes) +
+  if (plan->workspace_bytes <= 0 || plan->workspace_bytes > (int64_t)FFA_NOALLOC_MAX_BYTES)
+    return fail(FFA_E_SIZE, "batch needs " + std::to_string(plan->workspace_bytes) +
                                 " bytes of device scratch; the allocation-free entry holds at most " +
                                 std::to_string((int64_t)FFA_NOALLOC_MAX_BYTES) + " (use ffa_align_launch)");
   int device = -1;
@@ -2724,9 +2820,7 @@ extern "C" int ffa_align_launch_noalloc(const ffa_align_plan* plan, const ffa_al
   const int rc = scratch_address(device, &base);
   if (rc != FFA_OK) return rc;
   // nothing in the workspace has to start at zero: every kernel writes what it reads
-  err = hipMemcpyAsync(base, host_table, plan->table_bytes, hipMemcpyHostToDevice, stream);
-  if (err != hipSuccess) return fail(FFA_E_HIP, std::string("descriptor upload failed: ") + hipGetErrorString(err));
-  return ffa_align_launch(plan, o, base, emission_validity, out, base + table, stream);
+  return ffa_align_launch(plan, o, host_table, emission_validity, out, base, stream);
 }
 
 extern "C" int ffa_token_spans_launch(const ffa_span_record* device_records, int64_t count, const int64_t* labels,

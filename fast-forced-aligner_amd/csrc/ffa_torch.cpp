@@ -9,10 +9,11 @@
 // twenty arguments.
 //
 // Both entry points share one implementation that only adapts tensors to the
-// C ABI of include/ffa.h: it checks arguments, writes the descriptor table into
-// pinned host memory and uploads it asynchronously, allocates the scratch and
-// the outputs from PyTorch's caching allocator (one block each), and enqueues
-// the HIP kernels on the current stream. It never synchronizes the host.
+// C ABI of include/ffa.h: it checks arguments, writes the descriptor table
+// (passed in the kernel arguments, or uploaded from pinned host memory for
+// batches of more than 64 records), allocates the scratch and the outputs from
+// PyTorch's caching allocator (one block each), and enqueues the HIP kernels on
+// the current stream. It never synchronizes the host.
 #include <ATen/ATen.h>
 #include <ATen/core/CachingHostAllocator.h>
 #include <ATen/hip/impl/HIPCachingAllocatorMasqueradingAsCUDA.h>
@@ -113,19 +114,25 @@ std::tuple<std::vector<at::Tensor>, std::vector<int64_t>> run_align(int64_t coun
   }
   ffa_align_plan plan;
   check_ffa(ffa_align_plan_batch(records.data(), count, &o, &plan));
-  // descriptor table: pinned host block, uploaded on the stream into the head
-  // of the scratch allocation; the block is not reused before the copy ran
-  auto* host_alloc = at::getHostAllocator(at::kCUDA);
-  c10::DataPtr host = host_alloc->allocate(plan.table_bytes);
-  check_ffa(ffa_align_describe(&plan, records.data(), host.get(), plan.table_bytes));
-  const int64_t table_bytes = align256(plan.table_bytes);
+  // descriptor table: batches of at most FFA_TABLE_ARG_RECORDS records pass it
+  // in the kernel arguments (a host buffer reused once the launch returns);
+  // larger ones are uploaded by the launch from a pinned block, which must not
+  // be reused before the copy ran
+  thread_local std::vector<unsigned char> arg_table;
+  c10::DataPtr host;
+  void* table = nullptr;
+  at::HostAllocator* host_alloc = nullptr;
+  if (plan.table_uploaded) {
+    host_alloc = at::getHostAllocator(at::kCUDA);
+    host = host_alloc->allocate(plan.table_bytes);
+    table = host.get();
+  } else {
+    arg_table.resize(plan.table_bytes);
+    table = arg_table.data();
+  }
+  check_ffa(ffa_align_describe(&plan, records.data(), table, plan.table_bytes));
   const auto options = e0.options();
-  auto scratch = at::empty({table_bytes + plan.workspace_bytes}, options.dtype(at::kByte));
-  auto* scratch_ptr = static_cast<uint8_t*>(scratch.data_ptr());
-  const hipError_t copied = hipMemcpyAsync(scratch_ptr, host.get(), plan.table_bytes, hipMemcpyHostToDevice,
-                                           stream.stream());
-  TORCH_CHECK(copied == hipSuccess, "fast_forced_aligner: descriptor upload failed: ", hipGetErrorString(copied));
-  host_alloc->record_event(host.get(), host.get_context(), stream.unwrap());
+  auto scratch = at::empty({plan.workspace_bytes}, options.dtype(at::kByte));
   // outputs: one allocation, ten views (alignment.cu:1059 order)
   const int64_t N = plan.total_frames, B = count, R = plan.reuse_rows;
   int64_t off = 0;
@@ -156,7 +163,8 @@ std::tuple<std::vector<at::Tensor>, std::vector<int64_t>> run_align(int64_t coun
   out.shortcut_stats = reinterpret_cast<int64_t*>(base + o_shortcut);
   out.routing_stats = reinterpret_cast<int32_t*>(base + o_routing);
   out.reuse_stats = R ? reinterpret_cast<int64_t*>(base + o_reuse) : nullptr;
-  check_ffa(ffa_align_launch(&plan, &o, scratch_ptr, mask, &out, scratch_ptr + table_bytes, stream.stream()));
+  check_ffa(ffa_align_launch(&plan, &o, table, mask, &out, scratch.data_ptr(), stream.stream()));
+  if (plan.table_uploaded) host_alloc->record_event(host.get(), host.get_context(), stream.unwrap());
   return {{labels, scores, status, objective, stitched, repair_passes, repaired_frames, shortcut_stats,
            routing_stats, reuse_stats},
           std::move(sizes)};

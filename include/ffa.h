@@ -38,6 +38,7 @@ extern "C" {
 #define FFA_MAX_BATCH 65535      /* alignment.cu:979, alignment.py:237 */
 #define FFA_MAX_VOCAB 8192       /* alignment.cu:970, alignment.py:249 */
 #define FFA_MAX_STATES 20479     /* 2U+1; the reference stops at 4096 (alignment.cu:970) */
+#define FFA_TABLE_ARG_RECORDS 64 /* batches up to this size pass their record table as a kernel argument */
 
 /* One record of the ragged batch (alignment.cu:961-988 reads the same facts
  * from each tensor pair). */
@@ -82,8 +83,12 @@ typedef struct ffa_align_options {
 typedef struct ffa_align_plan {
   int64_t count;            /* B */
   int64_t total_frames;     /* N = sum of T: length of labels and scores */
-  int64_t table_bytes;      /* descriptor table; filled on the host, copied to the device */
-  int64_t workspace_bytes;  /* device scratch for one call */
+  int64_t table_bytes;      /* descriptor table, written on the host by ffa_align_describe */
+  int64_t table_uploaded;   /* 0: the table travels in the kernel arguments (B <= FFA_TABLE_ARG_RECORDS)
+                               and may be reused as soon as ffa_align_launch returns; 1: ffa_align_launch
+                               copies it into the workspace on the stream, so it must stay unchanged until
+                               the stream reaches the work (pinned memory keeps the copy asynchronous) */
+  int64_t workspace_bytes;  /* device scratch for one call (the table's device copy included) */
   int64_t reuse_rows;       /* rows of reuse_stats: B when frontier reuse is active, else 0 */
   int64_t internal[24];     /* launch geometry; read by ffa_align_launch only */
 } ffa_align_plan;
@@ -112,30 +117,30 @@ void ffa_default_options(int optimized, ffa_align_options* options);
 int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_align_options* options,
                          ffa_align_plan* plan);
 
-/* Writes the descriptor table into host memory (pinned memory lets the caller
- * upload it asynchronously, as alignment.cu:1005 does). */
+/* Writes the descriptor table into host memory (the per-record metadata that
+ * alignment.cu:996-1005 writes into pinned memory and uploads). */
 int ffa_align_describe(const ffa_align_plan* plan, const ffa_record* records,
                        void* host_table, int64_t host_table_bytes);
 
-/* Enqueues the alignment: replaces the kernel sequence of alignment.cu:1044-1053
- * (pack_inputs + launch_alignment). device_table holds the bytes written by
- * ffa_align_describe; emission_validity is an optional device bool[B] mask
- * (alignment.cu:946-952); workspace holds plan->workspace_bytes. */
+/* Enqueues the alignment: replaces the descriptor upload and the kernel
+ * sequence of alignment.cu:1005-1053 (pack_inputs + launch_alignment).
+ * host_table holds the bytes written by ffa_align_describe (see
+ * plan->table_uploaded for how long it must live); emission_validity is an
+ * optional device bool[B] mask (alignment.cu:946-952); workspace is device
+ * memory of plan->workspace_bytes. */
 int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_options* options,
-                     const void* device_table, const uint8_t* emission_validity,
+                     const void* host_table, const uint8_t* emission_validity,
                      const ffa_align_outputs* outputs, void* workspace, hipStream_t stream);
 
 /* Allocation-free variant of ffa_align_launch. No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
- * The descriptor table and the workspace live in a device array of
+ * The workspace (with the table's device copy) lives in a device array of
  * FFA_NOALLOC_MAX_BYTES that the library holds on each GPU it runs on until the
- * process ends; host_table (the bytes ffa_align_describe wrote, best in pinned
- * memory, kept unchanged until the stream reaches the work) is copied into it
- * on `stream`. The caller passes inputs and outputs as for ffa_align_launch;
- * `stream` must belong to the current device. Nothing is allocated or freed.
- * Returns FFA_E_SIZE when the plan's table (rounded up to 256 bytes) plus its
- * workspace exceed FFA_NOALLOC_MAX_BYTES (32 MiB: about 12 MiB serves 64
+ * process ends. The caller passes the host table, inputs and outputs as for
+ * ffa_align_launch; `stream` must belong to the current device. Nothing is
+ * allocated or freed. Returns FFA_E_SIZE when plan->workspace_bytes exceeds
+ * FFA_NOALLOC_MAX_BYTES (32 MiB: about 12 MiB serves 64
  * records of 250..1,750 frames and ~500 tokens; four 30,000-frame records of
  * 9,000 tokens need 580 MiB and must use ffa_align_launch).
  * Every call on a GPU shares that GPU's array: calls enqueued on one stream

@@ -76,10 +76,13 @@ def test_plan_sizes_and_gating(lib):
     rc, plan, recs = _plan(lib, [(500, 32, 4, 0), (320, 32, 3, 0)])
     assert rc == 0
     assert plan.count == 2 and plan.total_frames == 820
-    slots = 4 + 3  # ceil(T/128)
-    # 64-byte record descriptors and 16-byte chunk entries
-    assert plan.table_bytes == 2 * 64 + 16 * slots
+    # 64-byte record descriptors, passed as a kernel argument
+    assert plan.table_bytes == 2 * 64 and plan.table_uploaded == 0
     assert plan.reuse_rows == 0
+    # more than 64 records: descriptors plus one 16-byte entry per chunk, uploaded
+    rc, big, _ = _plan(lib, [(500, 32, 4, 0)] * 65)
+    assert rc == 0 and big.table_uploaded == 1 and big.table_bytes == 65 * 64 + 65 * 4 * 16
+    assert big.workspace_bytes >= big.table_bytes
     rc, plan, _ = _plan(lib, [(2048, 32, 4, 0), (320, 32, 3, 0)])
     assert rc == 0 and plan.reuse_rows == 2  # frontier reuse: batch max T >= 2048 (alignment.cu:1002)
     rc, plan, _ = _plan(lib, [(2048, 32, 4, 0)], optimized=False)
@@ -89,8 +92,8 @@ def test_plan_sizes_and_gating(lib):
     assert lib.ffa_align_describe(ctypes.byref(plan), recs, buf, plan.table_bytes - 1) == -3
     buf = (ctypes.c_uint8 * plan.table_bytes)()
     assert lib.ffa_align_describe(ctypes.byref(plan), recs, buf, plan.table_bytes) == 0
-    words = (ctypes.c_int64 * 8).from_buffer(buf)
-    assert (words[2], words[3]) == (50, 0)  # frames, frame offset
+    words = (ctypes.c_int32 * 16).from_buffer(buf)
+    assert (words[4], words[5], words[6], words[7], words[8], words[9]) == (50, 0, 8, 2, 0, 0)  # T, chunk, V, U, frame offset
 
 
 @pytest.mark.parametrize("shape, changes, message", [
@@ -128,11 +131,15 @@ def test_plan_rejects_target_addresses_the_chunk_entries_cannot_hold(lib, addres
 
 
 def test_chunk_entries_hold_targets_address_and_counts(lib):
-    rc, plan, recs = _plan(lib, [(300, 32, 5, 0)])
-    assert rc == 0
+    """Uploaded tables (more than 64 records) carry one 16-byte entry per chunk
+    after the record descriptors; tables passed as kernel arguments have none."""
+    rc, small, _ = _plan(lib, [(300, 32, 5, 0)])
+    assert rc == 0 and small.table_uploaded == 0 and small.table_bytes == 64
+    rc, plan, recs = _plan(lib, [(300, 32, 5, 0)] + [(10, 8, 1, 0)] * 64)
+    assert rc == 0 and plan.table_uploaded == 1
     buf = (ctypes.c_uint8 * plan.table_bytes)()
     assert lib.ffa_align_describe(ctypes.byref(plan), recs, buf, plan.table_bytes) == 0
-    entries = (ctypes.c_uint64 * 6).from_buffer(buf, 64)  # after the one 64-byte record descriptor
+    entries = (ctypes.c_uint64 * 6).from_buffer(buf, 65 * 64)  # after the 65 record descriptors
     for c in range(3):  # 300 frames: chunks of 128, 128, 44
         lo, hi = entries[2 * c], entries[2 * c + 1]
         assert (lo & ((1 << 45) - 1)) << 3 == recs[0].targets

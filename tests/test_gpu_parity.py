@@ -236,9 +236,8 @@ def test_c_abi_direct_call():
         o = capi.default_options(lib, optimized)
         plan = capi.Plan()
         capi.check(lib, lib.ffa_align_plan_batch(recs, 2, ctypes.byref(o), ctypes.byref(plan)))
-        host = torch.empty(plan.table_bytes, dtype=torch.uint8).pin_memory()
+        host = torch.empty(plan.table_bytes, dtype=torch.uint8)
         capi.check(lib, lib.ffa_align_describe(ctypes.byref(plan), recs, host.data_ptr(), plan.table_bytes))
-        table = host.to(DEV)
         N, B = plan.total_frames, 2
         outs = {"labels": torch.empty(N, dtype=torch.int64, device=DEV),
                 "scores": torch.empty(N, dtype=torch.float32, device=DEV),
@@ -253,7 +252,7 @@ def test_c_abi_direct_call():
         out = capi.Outputs(*[outs[f].data_ptr() if outs[f].numel() else None for f in FIELDS])
         ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=DEV)
         stream = torch.cuda.current_stream().cuda_stream
-        capi.check(lib, lib.ffa_align_launch(ctypes.byref(plan), ctypes.byref(o), table.data_ptr(), None,
+        capi.check(lib, lib.ffa_align_launch(ctypes.byref(plan), ctypes.byref(o), host.data_ptr(), None,
                                              ctypes.byref(out), ws.data_ptr(), stream))
         torch.cuda.synchronize()
         got = {f: outs[f].cpu().numpy() for f in FIELDS}

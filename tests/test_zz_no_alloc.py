@@ -53,9 +53,8 @@ def _run(lib, es, ys, optimized, noalloc):
         capi.check(lib, lib.ffa_align_launch_noalloc(ctypes.byref(plan), ctypes.byref(o), host.data_ptr(), None,
                                                      ctypes.byref(ptrs), stream))
     else:
-        table = host.to(DEV)
         ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=DEV)
-        capi.check(lib, lib.ffa_align_launch(ctypes.byref(plan), ctypes.byref(o), table.data_ptr(), None,
+        capi.check(lib, lib.ffa_align_launch(ctypes.byref(plan), ctypes.byref(o), host.data_ptr(), None,
                                              ctypes.byref(ptrs), ws.data_ptr(), stream))
     torch.cuda.synchronize()
     return {f: outs[f].cpu().numpy() for f in FIELDS}
