@@ -305,6 +305,28 @@ def cpu_baseline(batch, seconds=10.0):
                       f"one record per task on {cores} threads"}
 
 
+def line_bound(name: str) -> dict:
+    """Line-granular HBM lower bound of a config's greedy reads: per record and
+    frame, every L2 line (128 B) or memory sector (64 / 32 B) of the row that
+    holds a transcript-alphabet column is fetched whole, plus the int64 label
+    and fp32 score written per frame and the targets read once. Host only."""
+    import numpy as np
+
+    from fast_forced_aligner import workloads
+
+    batch = workloads.make(name)
+    lines = {128: 0, 64: 0, 32: 0}
+    frames = 0
+    for e, y in zip(batch.emissions, batch.targets):
+        cols = np.unique(np.r_[y, 0])
+        for g in lines:
+            lines[g] += e.shape[0] * len(np.unique(cols // (g // 4))) * g
+        frames += e.shape[0]
+    rest = 12 * frames + 8 * sum(int(y.size) for y in batch.targets)
+    return {"config": name, "algorithmic_bytes": batch.min_bytes(),
+            **{f"bound_{g}B_lines": v + rest for g, v in lines.items()}}
+
+
 def matrix(path: str) -> int:
     """Every config of BASELINE.json in both modes, with and without
     check_inputs, by the reference's timing contract (benchmarks/README.md:
@@ -390,6 +412,8 @@ def main() -> int:
     parser.add_argument("--matrix", metavar="PATH",
                         help="instead of the bench line: measure every config in both modes (single-call and "
                              "pipelined times, kernel, roofline, parity, CPU baseline) and write a markdown table")
+    parser.add_argument("--line-bound", metavar="CONFIG",
+                        help="print the line-granular HBM lower bound of CONFIG's greedy reads and exit (host only)")
     parser.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                         help="after the timed work, run 10 plain device copies of MIB MiB (a known-size "
                              "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE counter passes)")
@@ -401,6 +425,9 @@ def main() -> int:
         return 2
     if args.matrix:
         return matrix(args.matrix)
+    if args.line_bound:
+        print(json.dumps(line_bound(args.line_bound)))
+        return 0
 
     import numpy as np
     import torch
