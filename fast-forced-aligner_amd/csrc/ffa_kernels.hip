@@ -198,7 +198,18 @@ __device__ inline size_t align16(size_t x) { return (x + 15) & ~size_t(15); }
 // (the fast path indexes them by lane across two waves).
 __host__ __device__ inline int64_t greedy_frames(int64_t H) { return H < 128 ? 128 : (H + 31) & ~int64_t(31); }
 
-__device__ inline Lds carve(unsigned char* base, const Params& p) {
+// The sizes that fix the LDS layout (a subset of Params).
+struct LdsShape {
+  int32_t u_cap, eblk_frames, H, d_cap, v_words;
+};
+
+__device__ inline Lds carve(unsigned char* base, const Params& p);
+
+__device__ inline LdsShape lds_shape(const Params& p) {
+  return LdsShape{p.u_cap, p.eblk_frames, p.H, p.d_cap, p.v_words};
+}
+
+__device__ inline Lds carve(unsigned char* base, const LdsShape& p) {
   Lds L;
   size_t off = 0;
   L.h = reinterpret_cast<Header*>(base);
@@ -228,6 +239,8 @@ __device__ inline Lds carve(unsigned char* base, const Params& p) {
   L.tslots = reinterpret_cast<Slot*>(region);
   return L;
 }
+
+__device__ inline Lds carve(unsigned char* base, const Params& p) { return carve(base, lds_shape(p)); }
 
 // Pointers read from the descriptor table or the parameter block are generic
 // to the compiler, which would emit flat accesses; flat loads also count
@@ -1780,6 +1793,32 @@ __device__ inline int xcd_slot(int bid, int total) {
 __device__ inline Slot load_slot(const Slot* x) { return *x; }
 __device__ inline Slot load_slot(const GLB Slot* x) { return load_pod(x); }
 
+// The tail kernel's repair and fallback DPs. For K = 32 (transcripts of more
+// than 8,192 states) they run in a function of their own: the tail's repair
+// bookkeeping then costs no registers inside the frame loop, which gets the
+// conventional kernel's loop form and register budget (inlined into the tail,
+// the K = 32 frame loop spilled 12 to 30 registers per frame). The LDS view is
+// rebuilt inside from the kernel's dynamic shared memory (not passed in), so
+// that its pointers stay LDS pointers to the compiler.
+template <int K, int D, bool LG>
+__device__ __attribute__((noinline)) DPOut tail_dp_k32(const Rec& r, LdsShape shape, int64_t a, int64_t b,
+                                                        bool record_end, const GLB float* resume_from,
+                                                        int64_t start_t, GLB float* save_frontier, int trace) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  const Lds L = carve(lds_raw, shape);
+  return dp_interval<K, D, LG, false>(r, L, a, b, record_end, resume_from, start_t, save_frontier, trace);
+}
+
+template <int K, int D, bool LG>
+__device__ __attribute__((always_inline)) DPOut tail_dp(const Params& p, const Rec& r, const Lds& L, int64_t a,
+                                                         int64_t b, bool record_end, const GLB float* resume_from,
+                                                         int64_t start_t, GLB float* save_frontier, int trace) {
+  if constexpr (K == 32)
+    return tail_dp_k32<K, D, LG>(r, lds_shape(p), a, b, record_end, resume_from, start_t, save_frontier, trace);
+  else
+    return dp_interval<K, D, LG>(r, L, a, b, record_end, resume_from, start_t, save_frontier, trace);
+}
+
 // The tail of one record; SP is the slot array, in LDS or in global memory.
 template <int K, int D, bool LG, class SP>
 __device__ __attribute__((always_inline)) void tail_body(const Params& p, const RecordDesc& d, int rec, const Rec& r,
@@ -1928,7 +1967,7 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
         const Slot s0 = load_slot(sl + (0));
         const bool resume = frontier_on && s0.frontier_end > 0 && s0.frontier_end <= T;
         if (resume && tid == 0) { ts.reuse[1] += s0.frontier_end; ts.reuse[3] += S; }
-        const DPOut o = dp_interval<K, D, LG>(r, L, 0, T, true, resume ? r.frontier : nullptr,
+        const DPOut o = tail_dp<K, D, LG>(p, r, L, 0, T, true, resume ? r.frontier : nullptr,
                                           resume ? s0.frontier_end : 1, nullptr, TRACE_IF_FINITE);
         status = isfinite(o.score) ? 0 : 1;
         objective = o.score;
@@ -1951,7 +1990,7 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
           }
           if (tid == 0) ts.reuse[2] += S;
         }
-        const DPOut o = dp_interval<K, D, LG>(r, L, s.a, s.b, s.b == T, resume ? fr : nullptr, start_t, fr,
+        const DPOut o = tail_dp<K, D, LG>(p, r, L, s.a, s.b, s.b == T, resume ? fr : nullptr, start_t, fr,
                                           TRACE_ALWAYS);
         if (tid == 0) {
           sl[k].objective = o.score;
@@ -1991,7 +2030,7 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
       const Slot s0 = load_slot(sl + (0));
       const bool resume = frontier_on && s0.frontier_end > 0 && s0.frontier_end <= T;
       if (resume && tid == 0) { ts.reuse[1] += s0.frontier_end; ts.reuse[3] += S; }
-      const DPOut o = dp_interval<K, D, LG>(r, L, 0, T, true, resume ? r.frontier : nullptr,
+      const DPOut o = tail_dp<K, D, LG>(p, r, L, 0, T, true, resume ? r.frontier : nullptr,
                                         resume ? s0.frontier_end : 1, nullptr, TRACE_IF_FINITE);
       status = isfinite(o.score) ? 0 : 1;
       objective = o.score;
