@@ -61,9 +61,16 @@ struct RecordDesc {
   int64_t frame_offset;     // into labels / scores
   int64_t bp_offset;        // 32-bit words into the backpointer scratch
   int64_t frontier_offset;  // floats into the frontier scratch; -1 when unused
-  int32_t blank, pad;
+  int32_t blank;
+  int32_t flags;            // DESC_REUSE_COUNTED
 };
 static_assert(sizeof(RecordDesc) == 64, "descriptor layout");
+// The record is one the reference would run with frontier reuse (T >=
+// frontier_min_frames in a batch that enables it, alignment.cu:374): its
+// reuse_stats row counts frontier writes and resumed frames. Records without
+// the flag still save and resume frontiers when storage exists; results are
+// the same either way.
+constexpr int32_t DESC_REUSE_COUNTED = 1;
 
 // The record table passed by value as a kernel argument (batches of at most
 // FFA_TABLE_ARG_RECORDS records): the runtime copies it with the launch, so
@@ -1843,7 +1850,8 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
   }
   load_tokens(r, L.ytok);
   const int S = r.S;
-  const bool frontier_on = r.frontier != nullptr;
+  const bool frontier_on = r.frontier != nullptr;  // frontiers are saved and resumed
+  const bool counted = frontier_on && (d.flags & DESC_REUSE_COUNTED);  // and show in reuse_stats
   // Fast path (records of at most 64 chunks, slots in LDS): when every chunk
   // objective is finite and every seam is legal, the repair rounds merge
   // nothing (plan_repairs joins every neighbour and its budget preflight
@@ -1880,7 +1888,7 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
             for (int q = 0; q < 3; ++q) glb(p.routing_stats)[3 * rec + q] = 0;
             if (p.reuse_stats) {
               GLB int64_t* u = glb(p.reuse_stats) + 4 * rec;
-              u[0] = 0; u[1] = 0; u[2] = frontier_on ? (int64_t)__popcll(dp) * S : 0; u[3] = 0;
+              u[0] = 0; u[1] = 0; u[2] = counted ? (int64_t)__popcll(dp) * S : 0; u[3] = 0;
             }
           }
         }
@@ -1898,7 +1906,7 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
       if (sl[k].kind == 1) { ++ts.sc_accepted; ts.sc_frames += sl[k].b - sl[k].a; }
       else {
         if (sl[k].kind == 2) ++ts.sc_ambiguous;
-        if (frontier_on) ts.reuse[2] += S;
+        if (counted) ts.reuse[2] += S;
       }
     }
   }
@@ -1966,7 +1974,7 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
       if (early == 1) {  // early full fallback (repair_recurrence, cu:535-550)
         const Slot s0 = load_slot(sl + (0));
         const bool resume = frontier_on && s0.frontier_end > 0 && s0.frontier_end <= T;
-        if (resume && tid == 0) { ts.reuse[1] += s0.frontier_end; ts.reuse[3] += S; }
+        if (resume && counted && tid == 0) { ts.reuse[1] += s0.frontier_end; ts.reuse[3] += S; }
         const DPOut o = tail_dp<K, D, LG>(p, r, L, 0, T, true, resume ? r.frontier : nullptr,
                                           resume ? s0.frontier_end : 1, nullptr, TRACE_IF_FINITE);
         status = isfinite(o.score) ? 0 : 1;
@@ -1986,9 +1994,9 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
           if (s.frontier_end > s.a && s.frontier_end <= s.b) {
             resume = true;
             start_t = s.frontier_end;
-            if (tid == 0) { ts.reuse[0] += s.frontier_end - s.a; ts.reuse[3] += S; }
+            if (tid == 0 && counted) { ts.reuse[0] += s.frontier_end - s.a; ts.reuse[3] += S; }
           }
-          if (tid == 0) ts.reuse[2] += S;
+          if (tid == 0 && counted) ts.reuse[2] += S;
         }
         const DPOut o = tail_dp<K, D, LG>(p, r, L, s.a, s.b, s.b == T, resume ? fr : nullptr, start_t, fr,
                                           TRACE_ALWAYS);
@@ -2029,7 +2037,7 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
     if (!stitched) {  // fallback_recurrence, cu:552-559
       const Slot s0 = load_slot(sl + (0));
       const bool resume = frontier_on && s0.frontier_end > 0 && s0.frontier_end <= T;
-      if (resume && tid == 0) { ts.reuse[1] += s0.frontier_end; ts.reuse[3] += S; }
+      if (resume && counted && tid == 0) { ts.reuse[1] += s0.frontier_end; ts.reuse[3] += S; }
       const DPOut o = tail_dp<K, D, LG>(p, r, L, 0, T, true, resume ? r.frontier : nullptr,
                                         resume ? s0.frontier_end : 1, nullptr, TRACE_IF_FINITE);
       status = isfinite(o.score) ? 0 : 1;
@@ -2106,7 +2114,7 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p, TB
     d.bp_offset = rd.bp_offset;
     d.frontier_offset = rd.frontier_offset;
     d.blank = rd.blank;
-    d.pad = 0;
+    d.flags = rd.flags;
   } else {
     const ChunkEntry ce = load_uniform(p.chunks + slot_index);
     rec = (int)(ce.hi & 0xffffu);
@@ -2246,7 +2254,7 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) tail_kernel(Params p) {
       const Slot sk = load_pod(gs + (valid ? k : 0));
       const int status0 = __builtin_amdgcn_readfirstlane(sk.status);
       const int S = 2 * d.tokens + 1;
-      const bool frontier_on = d.frontier_offset >= 0;
+      const bool counted = d.frontier_offset >= 0 && (d.flags & DESC_REUSE_COUNTED);
       int done = 0;
       if (status0 >= 2) {  // rejected record: every chunk wrote -1 / -inf
         done = 1;
@@ -2290,7 +2298,7 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) tail_kernel(Params p) {
               for (int q = 0; q < 3; ++q) glb(p.routing_stats)[3 * rec + q] = 0;
               if (p.reuse_stats) {
                 GLB int64_t* u = glb(p.reuse_stats) + 4 * rec;
-                u[0] = 0; u[1] = 0; u[2] = frontier_on ? (int64_t)__popcll(dp) * S : 0; u[3] = 0;
+                u[0] = 0; u[1] = 0; u[2] = counted ? (int64_t)__popcll(dp) * S : 0; u[3] = 0;
               }
             }
           }
@@ -2492,6 +2500,15 @@ int launch_geometry(const ffa::Params& p, const TB& tab, int NT, size_t lds, boo
 int states_of(const ffa_record& r) { return (int)(2 * r.tokens + 1); }
 int64_t stride_of(int S) { return 2 * (((int64_t)S + 31) / 32); }
 
+// Frontier storage beyond the reference's gating (alignment.cu:374, T >=
+// frontier_min_frames): in optimized mode with chunks of at least 32 frames
+// every record keeps one frontier per chunk (S floats, at most an eighth of its
+// backpointer bytes), so a repair that starts where a chunk DP started, and a
+// fallback after a repair from frame 0, resume instead of recomputing those
+// frames. A resumed DP gives the same values as a fresh one, so only
+// reuse_stats follows the reference's gating.
+bool frontier_for_every_record(bool optimized, int64_t H) { return optimized && H >= 32; }
+
 // The 2-bit backpointer row of a record is 2*ceil(S/32) words; K contiguous
 // states per thread. K = 4, 8 or 16 keep a record in at most 4 waves (one per
 // SIMD); wider transcripts take K = 32 and up to 10 waves.
@@ -2603,10 +2620,10 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
   if (slots > INT_MAX || bp_words < 0) return fail(FFA_E_INVALID, "chunk endpoints or interval indices exceed int32 range");
   const bool budget_on = max_frames >= o->repair_min_frames;  // alignment.cu:993-996
   const bool frontier = optimized && o->frontier_reuse && max_frames >= o->frontier_min_frames;  // :935, :1002
-  if (frontier)
-    for (int64_t i = 0; i < count; ++i)
-      if (records[i].frames >= o->frontier_min_frames)
-        frontier_floats += (1 + (records[i].frames - 1) / H) * (int64_t)states_of(records[i]);
+  const bool store_all = frontier_for_every_record(optimized, H);
+  for (int64_t i = 0; i < count; ++i)
+    if (store_all || (frontier && records[i].frames >= o->frontier_min_frames))
+      frontier_floats += (1 + (records[i].frames - 1) / H) * (int64_t)states_of(records[i]);
   int K, NT;
   geometry(s_max, &K, &NT);
   const int64_t v_words = (v_max + 31) / 32;
@@ -2682,6 +2699,7 @@ int ffa_align_describe(const ffa_align_plan* plan, const ffa_record* records, vo
   const int64_t H = in[I_H];
   auto* desc = static_cast<ffa::RecordDesc*>(host_table);
   auto* chunks = reinterpret_cast<ffa::ChunkEntry*>(desc + count);
+  const bool store_all = frontier_for_every_record(optimized, H);
   int64_t frame = 0, bp = 0, fr = 0;
   int32_t slot = 0;
   for (int64_t i = 0; i < count; ++i) {
@@ -2698,9 +2716,10 @@ int ffa_align_describe(const ffa_align_plan* plan, const ffa_record* records, vo
     d.bp_offset = bp;
     d.frontier_offset = -1;
     d.blank = (int32_t)r.blank;
-    d.pad = 0;
+    const bool counted = frontier && r.frames >= in[I_FMIN];  // alignment.cu:374
+    d.flags = counted ? ffa::DESC_REUSE_COUNTED : 0;
     const int64_t n = 1 + (r.frames - 1) / H;
-    if (frontier && r.frames >= in[I_FMIN]) {  // alignment.cu:374: per-record frontier storage
+    if (counted || store_all) {  // per-record frontier storage, one block of S floats per chunk
       d.frontier_offset = fr;
       fr += n * S;
     }
