@@ -595,38 +595,62 @@ __device__ inline void store_row(GLB uint32_t* row, int tid, typename BitsT<K>::
   }
 }
 
-// Path walk from (b-1, terminal) down to a by wave 0. Each batch loads, for up
-// to 64 frames at once (one per lane), the two backpointer words around the
-// current state, then resolves the steps serially from registers until the
-// state leaves that 32-state window. Writes labels and scores (finish,
-// cu:642-667) and returns the state at frame a.
+// Path walk from (b-1, terminal) down to a by wave 0 (finish, cu:642-667:
+// writes labels and scores; returns the state at frame a).
+//
+// Batches of up to 64 frames, one per lane: lane i holds the four backpointer
+// words (64 states) of frame t-i at and below the word of the batch's first
+// state. The steps are resolved in groups of 8 in scalar registers: a group
+// starts where the current state's word and the one below it are both in the
+// window, and 8 steps move at most 16 states, so the group reads only those
+// two words, joined into one 64-bit value (no bounds test per step). Each
+// step records its state into the lane of its frame. A batch ends after 64
+// frames or when the state has left the window; the next batch's words are
+// requested before this batch's labels and scores are written, so their
+// latency overlaps the stores and the score gathers.
 __device__ inline int trace_path(const Rec& r, int64_t a, int64_t b, int terminal) {
   const int lane = threadIdx.x & 63;
+  const int64_t stride = r.stride;
+  auto load_window = [&](int64_t t, int whi, uint32_t (&w)[4]) {
+    const int64_t ti = t - lane;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = 0;
+    if (ti >= a) {
+      const GLB uint32_t* row = r.bp + ti * stride;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (whi - j >= 0) w[j] = row[whi - j];
+    }
+  };
   int64_t t = b - 1;
   int s = terminal;
+  uint32_t w[4];  // w[j]: word whi - j of this lane's frame
+  load_window(t, s >> 4, w);
   while (t >= a) {
     const int whi = s >> 4;
-    uint32_t vhi = 0, vlo = 0;
-    const int64_t ti = t - lane;
-    if (ti >= a) {
-      const GLB uint32_t* row = r.bp + ti * (int64_t)r.stride;
-      vhi = row[whi];
-      if (whi > 0) vlo = row[whi - 1];
-    }
     const int lim = (int)min((int64_t)64, t - a + 1);
     int cur = s, steps = 0, mine = 0;
-    for (int i = 0; i < lim; ++i) {
-      const int w = cur >> 4;
-      const uint32_t hv = (uint32_t)__builtin_amdgcn_readlane((int)vhi, i);
-      const uint32_t lv = (uint32_t)__builtin_amdgcn_readlane((int)vlo, i);
-      uint32_t word;
-      if (w == whi) word = hv;
-      else if (w == whi - 1) word = lv;
-      else break;
-      if (lane == i) mine = cur;
-      cur -= (int)((word >> ((cur & 15) << 1)) & 3u);
-      steps = i + 1;
+    for (int g = 0; g < lim; g += 8) {
+      const int wsel = cur >> 4;
+      const int dw = whi - wsel;  // 0 .. 2 keep both words in the window
+      if (dw > 2) break;
+      const uint32_t vh = dw == 0 ? w[0] : dw == 1 ? w[1] : w[2];
+      const uint32_t vl = dw == 0 ? w[1] : dw == 1 ? w[2] : w[3];
+      const int base = (wsel - 1) * 16;  // state of bit pair 0 of {vh:vl}
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t hv = (uint32_t)__builtin_amdgcn_readlane((int)vh, g + j);
+        const uint32_t lv = (uint32_t)__builtin_amdgcn_readlane((int)vl, g + j);
+        const uint64_t word = (uint64_t)hv << 32 | lv;
+        mine = lane == g + j ? cur : mine;
+        cur -= (int)((word >> (2 * (cur - base))) & 3u);
+      }
+      // frames past the interval read zero words: their steps do not move
+      steps = min(g + 8, lim);
     }
+    const int64_t tn = t - steps;
+    uint32_t wn[4];
+    load_window(tn, cur >> 4, wn);
     if (lane < steps) {
       const int64_t tf = t - lane;
       const int lab = label_of(r, mine);
@@ -634,7 +658,9 @@ __device__ inline int trace_path(const Rec& r, int64_t a, int64_t b, int termina
       const float v = r.e[tf * r.V + lab];
       r.scores[tf] = r.st ? lsm(v, r.st[tf - r.st_first]) : v;
     }
-    t -= steps;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = wn[j];
+    t = tn;
     s = cur;
   }
   return s;
