@@ -140,7 +140,7 @@ int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_options* option
  * process ends. The caller passes the host table, inputs and outputs as for
  * ffa_align_launch; `stream` must belong to the current device. Nothing is
  * allocated or freed. Returns FFA_E_SIZE when plan->workspace_bytes exceeds
- * FFA_NOALLOC_MAX_BYTES (32 MiB: about 12 MiB serves 64
+ * FFA_NOALLOC_MAX_BYTES (32 MiB: about 14 MiB serves 64
  * records of 250..1,750 frames and ~500 tokens; four 30,000-frame records of
  * 9,000 tokens need 580 MiB and must use ffa_align_launch).
  * Every call on a GPU shares that GPU's array: calls enqueued on one stream
