@@ -598,72 +598,145 @@ __device__ inline void store_row(GLB uint32_t* row, int tid, typename BitsT<K>::
 // Path walk from (b-1, terminal) down to a by wave 0 (finish, cu:642-667:
 // writes labels and scores; returns the state at frame a).
 //
-// Batches of up to 64 frames, one per lane: lane i holds the four backpointer
-// words (64 states) of frame t-i at and below the word of the batch's first
-// state. The steps are resolved in groups of 8 in scalar registers: a group
-// starts where the current state's word and the one below it are both in the
-// window, and 8 steps move at most 16 states, so the group reads only those
-// two words, joined into one 64-bit value (no bounds test per step). Each
-// step records its state into the lane of its frame. A batch ends after 64
-// frames or when the state has left the window; the next batch's words are
-// requested before this batch's labels and scores are written, so their
-// latency overlaps the stores and the score gathers.
-__device__ inline int trace_path(const Rec& r, int64_t a, int64_t b, int terminal) {
+// Batches of up to 64 frames, one per lane: lane i holds eight backpointer
+// words (128 states) of frame t-i, from the window's top word down. The walk
+// itself is serial and runs in scalar registers, in one of two forms chosen
+// per batch by how far the previous batch moved:
+//  * steps: groups of 8 frames; a group starts where the current state's word
+//    and the one below it are both in the window (8 steps move at most 16
+//    states) and resolves its steps from those two words joined into one
+//    64-bit value, with the bit offset carried from step to step (no test or
+//    branch per step); each step's state goes to its frame's lane. Halfway
+//    through a full batch the next batch's words are requested around the
+//    current state;
+//  * runs (sparse paths, fewer than 8 state changes in the previous batch):
+//    every lane reads its frame's move at the current state, a ballot finds
+//    the first frame that moves, the frames up to it take the current state,
+//    and the state then takes that frame's move: one round per state change
+//    instead of one per frame. The next batch's words are requested when the
+//    batch starts, with the same top word.
+// A batch whose state leaves its window ends there and requests a new one. A
+// batch's score gathers are stored during the next batch, so the walk does
+// not wait for them.
+__device__ __attribute__((always_inline)) inline int trace_path(const Rec& r, int64_t a, int64_t b, int terminal) {
   const int lane = threadIdx.x & 63;
   const int64_t stride = r.stride;
-  auto load_window = [&](int64_t t, int whi, uint32_t (&w)[4]) {
+  constexpr int WW = 8;  // words per lane
+  auto load_window = [&](int64_t t, int wb, uint32_t (&w)[WW]) {
     const int64_t ti = t - lane;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) w[j] = 0;
+    for (int j = 0; j < WW; ++j) w[j] = 0;
     if (ti >= a) {
       const GLB uint32_t* row = r.bp + ti * stride;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (whi - j >= 0) w[j] = row[whi - j];
+      for (int j = 0; j < WW; ++j)
+        if (wb - j >= 0) w[j] = row[wb - j];
     }
   };
   int64_t t = b - 1;
-  int s = terminal;
-  uint32_t w[4];  // w[j]: word whi - j of this lane's frame
-  load_window(t, s >> 4, w);
+  int cur = terminal;
+  int wb = cur >> 4;  // word of w[0]
+  uint32_t w[WW], wn[WW];
+  load_window(t, wb, w);
+  // score of the previous batch's frame of this lane, stored during the next batch
+  bool pend = false;
+  int64_t pend_tf = 0;
+  float pend_v = 0.0f;
+  float2 pend_st = make_float2(0.0f, 0.0f);
+  auto flush = [&] {
+    if (pend) r.scores[pend_tf] = r.st ? lsm(pend_v, pend_st) : pend_v;
+    pend = false;
+  };
+  bool runs = 8 * (int64_t)r.S < b - a;  // first batch: the record's states per frame
   while (t >= a) {
-    const int whi = s >> 4;
     const int lim = (int)min((int64_t)64, t - a + 1);
-    int cur = s, steps = 0, mine = 0;
-    for (int g = 0; g < lim; g += 8) {
-      const int wsel = cur >> 4;
-      const int dw = whi - wsel;  // 0 .. 2 keep both words in the window
-      if (dw > 2) break;
-      const uint32_t vh = dw == 0 ? w[0] : dw == 1 ? w[1] : w[2];
-      const uint32_t vl = dw == 0 ? w[1] : dw == 1 ? w[2] : w[3];
-      const int base = (wsel - 1) * 16;  // state of bit pair 0 of {vh:vl}
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t hv = (uint32_t)__builtin_amdgcn_readlane((int)vh, g + j);
-        const uint32_t lv = (uint32_t)__builtin_amdgcn_readlane((int)vl, g + j);
-        const uint64_t word = (uint64_t)hv << 32 | lv;
-        mine = lane == g + j ? cur : mine;
-        cur -= (int)((word >> (2 * (cur - base))) & 3u);
+    const bool full = lim == 64 && t - 64 >= a;  // a next batch of frames follows
+    const int from = cur;
+    int mine = 0, pos = 0, wbn = -1;
+    if (runs) {
+      if (full) {
+        wbn = wb;
+        load_window(t - 64, wbn, wn);
       }
-      // frames past the interval read zero words: their steps do not move
-      steps = min(g + 8, lim);
+      const uint64_t live = lim == 64 ? ~0ull : (1ull << lim) - 1;
+      int wsel = -1;
+      uint32_t x = 0;  // this lane's word holding the current state
+      bool flushed = false;
+      while (pos < lim) {
+        const int ws = cur >> 4;
+        if (ws != wsel) {
+          const int dw = wb - ws;
+          if (dw > WW - 1) break;  // the state left the window: the batch ends here
+          x = w[0];
+#pragma unroll
+          for (int j = 1; j < WW; ++j)
+            if (dw == j) x = w[j];
+          wsel = ws;
+        }
+        const uint32_t mv = (x >> (2 * (cur & 15))) & 3u;
+        const uint64_t moving = __ballot(mv != 0) & live & (~0ull << pos);
+        const int l = moving ? (int)__builtin_ctzll(moving) : lim - 1;  // last frame of the run
+        if (lane >= pos && lane <= l) mine = cur;
+        if (!flushed) { flush(); flushed = true; }
+        pos = l + 1;
+        if (!moving) break;
+        cur -= __builtin_amdgcn_readlane((int)mv, l);
+      }
+    } else {
+      for (int g = 0; g < lim; g += 8) {
+        const int wsel = cur >> 4;
+        const int dw = wb - wsel;  // w[dw] and w[dw + 1] hold the group's two words
+        if (dw > WW - 2) break;
+        uint32_t vh = w[0], vl = w[1];
+#pragma unroll
+        for (int j = 1; j <= WW - 2; ++j)
+          if (dw == j) { vh = w[j]; vl = w[j + 1]; }
+        int sh = 2 * (cur - (wsel - 1) * 16);  // bit offset of the state in {vh:vl}
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t hv = (uint32_t)__builtin_amdgcn_readlane((int)vh, g + j);
+          const uint32_t lv = (uint32_t)__builtin_amdgcn_readlane((int)vl, g + j);
+          const int mv = (int)(((uint64_t)hv << 32 | lv) >> sh) & 3;
+          mine = lane == g + j ? cur : mine;
+          cur -= mv;
+          sh -= 2 * mv;
+        }
+        // frames past the interval read zero words: their steps do not move
+        pos = min(g + 8, lim);
+        if (g == 0) flush();
+        if (g == 24 && full) {
+          wbn = cur >> 4;
+          load_window(t - 64, wbn, wn);
+        }
+      }
     }
+    const int steps = pos;
     const int64_t tn = t - steps;
-    uint32_t wn[4];
-    load_window(tn, cur >> 4, wn);
+    if (tn >= a) {
+      const int wfirst = cur >> 4;
+      if (steps == 64 && wbn >= 0 && wbn - wfirst <= WW - 2) {
+#pragma unroll
+        for (int j = 0; j < WW; ++j) w[j] = wn[j];
+        wb = wbn;
+      } else {
+        wb = wfirst;
+        load_window(tn, wb, w);
+      }
+    }
     if (lane < steps) {
       const int64_t tf = t - lane;
       const int lab = label_of(r, mine);
       r.labels[tf] = lab;
-      const float v = r.e[tf * r.V + lab];
-      r.scores[tf] = r.st ? lsm(v, r.st[tf - r.st_first]) : v;
+      pend = true;
+      pend_tf = tf;
+      pend_v = r.e[tf * r.V + lab];
+      if (r.st) pend_st = r.st[tf - r.st_first];
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) w[j] = wn[j];
+    runs = 8 * (from - cur) < steps;
     t = tn;
-    s = cur;
   }
-  return s;
+  flush();
+  return cur;
 }
 
 // How the frame loop knows whether the workgroup has several waves: fixed
