@@ -1899,28 +1899,49 @@ __device__ inline int xcd_slot(int bid, int total) {
 __device__ inline Slot load_slot(const Slot* x) { return *x; }
 __device__ inline Slot load_slot(const GLB Slot* x) { return load_pod(x); }
 
-// The tail kernel's repair and fallback DPs. For K = 32 (transcripts of more
-// than 8,192 states) they run in a function of their own: the tail's repair
-// bookkeeping then costs no registers inside the frame loop, which gets the
-// conventional kernel's loop form and register budget (inlined into the tail,
-// the K = 32 frame loop spilled 12 to 30 registers per frame). The LDS view is
-// rebuilt inside from the kernel's dynamic shared memory (not passed in), so
-// that its pointers stay LDS pointers to the compiler.
+// A value every lane of the wave holds alike, moved word by word into scalar
+// registers (function arguments arrive in vector registers).
+template <class T>
+__device__ inline T uniform(const T& x) {
+  static_assert(sizeof(T) % 4 == 0, "32-bit words");
+  int w[sizeof(T) / 4];
+  __builtin_memcpy(w, &x, sizeof(T));
+#pragma unroll
+  for (size_t i = 0; i < sizeof(T) / 4; ++i) w[i] = __builtin_amdgcn_readfirstlane(w[i]);
+  T out;
+  __builtin_memcpy(&out, w, sizeof(T));
+  return out;
+}
+
+// The chunk, repair and fallback DPs of the optimized-mode kernels. For K = 32
+// (transcripts of more than 8,192 states) they run in a function of their
+// own: the chunk kernel's greedy code and the tail's repair bookkeeping then
+// cost no registers inside the frame loop, which gets the conventional
+// kernel's loop form and register budget (inlined into the tail, the K = 32
+// frame loop spilled 12 to 30 registers per frame). The record view and the
+// interval arrive as arguments, in vector registers; they are moved into
+// scalar registers at entry, and the LDS view is rebuilt from the kernel's
+// dynamic shared memory (not passed in), so that its pointers stay LDS
+// pointers to the compiler.
 template <int K, int D, bool LG>
-__device__ __attribute__((noinline)) DPOut tail_dp_k32(const Rec& r, LdsShape shape, int64_t a, int64_t b,
-                                                        bool record_end, const GLB float* resume_from,
-                                                        int64_t start_t, GLB float* save_frontier, int trace) {
+__device__ __attribute__((noinline)) DPOut dp_k32(const Rec& rv, LdsShape shape, int64_t a, int64_t b,
+                                                   bool record_end, const GLB float* resume_from, int64_t start_t,
+                                                   GLB float* save_frontier, int trace) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
-  const Lds L = carve(lds_raw, shape);
-  return dp_interval<K, D, LG, false>(r, L, a, b, record_end, resume_from, start_t, save_frontier, trace);
+  const Lds L = carve(lds_raw, uniform(shape));
+  Rec r = uniform(rv);
+  r.ytok = L.ytok;  // the record's staged targets (the same LDS array, typed as LDS)
+  return dp_interval<K, D, LG, false>(r, L, uniform(a), uniform(b), uniform((int)record_end) != 0,
+                                      uniform(resume_from), uniform(start_t), uniform(save_frontier),
+                                      uniform(trace));
 }
 
 template <int K, int D, bool LG>
-__device__ __attribute__((always_inline)) DPOut tail_dp(const Params& p, const Rec& r, const Lds& L, int64_t a,
-                                                         int64_t b, bool record_end, const GLB float* resume_from,
-                                                         int64_t start_t, GLB float* save_frontier, int trace) {
+__device__ __attribute__((always_inline)) DPOut run_dp(const Params& p, const Rec& r, const Lds& L, int64_t a,
+                                                        int64_t b, bool record_end, const GLB float* resume_from,
+                                                        int64_t start_t, GLB float* save_frontier, int trace) {
   if constexpr (K == 32)
-    return tail_dp_k32<K, D, LG>(r, lds_shape(p), a, b, record_end, resume_from, start_t, save_frontier, trace);
+    return dp_k32<K, D, LG>(r, lds_shape(p), a, b, record_end, resume_from, start_t, save_frontier, trace);
   else
     return dp_interval<K, D, LG>(r, L, a, b, record_end, resume_from, start_t, save_frontier, trace);
 }
@@ -2074,7 +2095,7 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
         const Slot s0 = load_slot(sl + (0));
         const bool resume = frontier_on && s0.frontier_end > 0 && s0.frontier_end <= T;
         if (resume && counted && tid == 0) { ts.reuse[1] += s0.frontier_end; ts.reuse[3] += S; }
-        const DPOut o = tail_dp<K, D, LG>(p, r, L, 0, T, true, resume ? r.frontier : nullptr,
+        const DPOut o = run_dp<K, D, LG>(p, r, L, 0, T, true, resume ? r.frontier : nullptr,
                                           resume ? s0.frontier_end : 1, nullptr, TRACE_IF_FINITE);
         status = isfinite(o.score) ? 0 : 1;
         objective = o.score;
@@ -2097,7 +2118,7 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
           }
           if (tid == 0 && counted) ts.reuse[2] += S;
         }
-        const DPOut o = tail_dp<K, D, LG>(p, r, L, s.a, s.b, s.b == T, resume ? fr : nullptr, start_t, fr,
+        const DPOut o = run_dp<K, D, LG>(p, r, L, s.a, s.b, s.b == T, resume ? fr : nullptr, start_t, fr,
                                           TRACE_ALWAYS);
         if (tid == 0) {
           sl[k].objective = o.score;
@@ -2137,7 +2158,7 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
       const Slot s0 = load_slot(sl + (0));
       const bool resume = frontier_on && s0.frontier_end > 0 && s0.frontier_end <= T;
       if (resume && counted && tid == 0) { ts.reuse[1] += s0.frontier_end; ts.reuse[3] += S; }
-      const DPOut o = tail_dp<K, D, LG>(p, r, L, 0, T, true, resume ? r.frontier : nullptr,
+      const DPOut o = run_dp<K, D, LG>(p, r, L, 0, T, true, resume ? r.frontier : nullptr,
                                         resume ? s0.frontier_end : 1, nullptr, TRACE_IF_FINITE);
       status = isfinite(o.score) ? 0 : 1;
       objective = o.score;
@@ -2308,7 +2329,7 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p, TB
       if (p.mode == 2 && !fast) accepted = greedy_chunk(r, L, a, b, st.blank_in, out, &ambiguous);
       if (!accepted) {  // initial chunk DP (cu:721-726), relaxed init for a > 0
         GLB float* fr = r.frontier ? r.frontier + chunk * r.S : nullptr;
-        const DPOut o = dp_interval<K, D, LG>(r, L, a, b, b == r.T, nullptr, a + 1, fr, TRACE_ALWAYS);
+        const DPOut o = run_dp<K, D, LG>(p, r, L, a, b, b == r.T, nullptr, a + 1, fr, TRACE_ALWAYS);
         out.objective = o.score;
         out.end = o.terminal;
         out.start = o.start;
