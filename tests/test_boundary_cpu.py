@@ -148,6 +148,41 @@ def test_chunk_entries_hold_targets_address_and_counts(lib):
         assert hi & 0xFFFF == 0 and ((hi >> 16) & 0x1FF) + 1 == (128, 128, 44)[c] and hi >> 25 == c
 
 
+def _descriptors(lib, plan, recs):
+    buf = (ctypes.c_uint8 * plan.table_bytes)()
+    assert lib.ffa_align_describe(ctypes.byref(plan), recs, buf, plan.table_bytes) == 0
+    q = (ctypes.c_int64 * (8 * plan.count)).from_buffer(buf)
+    w = (ctypes.c_int32 * (16 * plan.count)).from_buffer(buf)
+    # 64-byte records: frontier offset at byte 48, the counted-reuse flag at byte 60
+    return [(q[8 * i + 6], w[16 * i + 15]) for i in range(plan.count)]
+
+
+def test_frontier_storage_and_reuse_counting(lib):
+    """Optimized mode with chunks of at least 32 frames keeps S floats per
+    chunk for every record (repairs and fallbacks resume from them); only the
+    records the reference runs with frontier reuse (batch max T >= 2048 and the
+    record's T >= frontier_min_frames, alignment.cu:374, :1002) carry the flag
+    that makes reuse_stats count. Conventional mode and short chunks keep none
+    beyond the reference's."""
+    shapes = [(2048, 32, 4, 0), (300, 32, 5, 0), (500, 32, 2, 0)]
+    rc, plan, recs = _plan(lib, shapes)
+    assert rc == 0 and plan.reuse_rows == 3
+    # 2048 frames: 16 chunks x 9 states; 300: 3 x 11; 500: 4 x 5
+    assert _descriptors(lib, plan, recs) == [(0, 1), (144, 0), (177, 0)]
+    rc, plan, recs = _plan(lib, shapes[1:])  # no record reaches 2048 frames: nothing counted
+    assert rc == 0 and plan.reuse_rows == 0
+    assert _descriptors(lib, plan, recs) == [(0, 0), (33, 0)]
+    rc, plan, recs = _plan(lib, shapes, frontier_reuse=0)  # reference reuse off: storage stays
+    assert rc == 0 and plan.reuse_rows == 0
+    assert _descriptors(lib, plan, recs) == [(0, 0), (144, 0), (177, 0)]
+    rc, plan, recs = _plan(lib, shapes, chunk_frames=16)  # short chunks: the reference's records only
+    assert rc == 0 and plan.reuse_rows == 3
+    assert _descriptors(lib, plan, recs) == [(0, 1), (-1, 0), (-1, 0)]
+    rc, plan, recs = _plan(lib, shapes, optimized=False)
+    assert rc == 0 and plan.reuse_rows == 0
+    assert _descriptors(lib, plan, recs) == [(-1, 0), (-1, 0), (-1, 0)]
+
+
 def test_operator_schemas_match_the_reference():
     torch.ops.load_library(str(alignment.TORCH_LIBRARY))
     for name, schema in REFERENCE_SCHEMAS.items():
