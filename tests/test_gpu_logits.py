@@ -166,6 +166,18 @@ def test_fused_long_records_use_tail_statistics(mode):
         assert fused.reuse_stats.shape == (2, 4)
 
 
+@pytest.mark.parametrize("mode", MODES)
+def test_fused_widest_transcripts(mode):
+    """More than 8,192 states (K = 32): the chunk DP, repairs and fallback run
+    in the non-inlined DP function, which reads the row statistics through the
+    record view (from LDS in the chunk kernel, from global memory in the tail)."""
+    b = workloads.c3(batch=2, frames=8300, tokens=2500, raw=True)
+    print(f"K = 32 logits {mode}", flush=True)
+    logits, targets = dev(b.emissions), dev(b.targets, np.int64)
+    fused, _ = fused_equals_materialized(logits, targets, mode=mode)
+    assert (fused.status == 0).all()
+
+
 def test_fused_mask_and_statuses():
     b = workloads.c5(batch=64, raw=True)
     logits, targets = dev(b.emissions), dev(b.targets, np.int64)
