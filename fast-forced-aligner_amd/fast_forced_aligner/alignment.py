@@ -10,7 +10,7 @@ from __future__ import annotations
 import ctypes
 import os
 from collections.abc import Sequence
-from dataclasses import dataclass
+from dataclasses import dataclass, fields
 from functools import lru_cache
 from pathlib import Path
 from typing import Literal
@@ -132,6 +132,18 @@ class AlignmentBatch:
         raise ValueError("; ".join(messages))
 
 
+_BATCH_FIELDS = tuple(f.name for f in fields(AlignmentBatch))
+
+
+def _batch(lengths: tuple[int, ...], tensors: Sequence[Tensor]) -> AlignmentBatch:
+    """``AlignmentBatch(lengths, *tensors)`` with one dict update instead of the
+    frozen dataclass's eleven ``object.__setattr__`` calls (the same instance;
+    the per-call host cost of ``align`` is a few microseconds)."""
+    out = object.__new__(AlignmentBatch)
+    out.__dict__.update(zip(_BATCH_FIELDS, (lengths, *tensors)))
+    return out
+
+
 def _metadata(emissions: Sequence[Tensor], targets: Sequence[Tensor],
               blank_id: int | Sequence[int]) -> list[int]:
     """Host-only metadata checks (py:233-252). Returns one blank per record.
@@ -227,12 +239,13 @@ def align(emissions: Sequence[Tensor], targets: Sequence[Tensor], *,
         raise TypeError("check_inputs must be bool")
     if not (emissions and isinstance(emissions[0], Tensor) and emissions[0].is_cuda):
         _metadata(emissions, targets, blank_id)  # raises the reference's ValueError for these inputs
-    load_extension()
+    if _native is None:
+        load_extension()
     # the native entry checks every record's metadata with the same messages
     # (O(B) in C++) and passes the fixed knob vector of py:496-501
     tensors, lengths = _native.align(emissions, targets, blank_id, mode == "optimized", check_inputs,
                                      emission_validity)
-    return AlignmentBatch(lengths, *tensors)
+    return _batch(lengths, tensors)
 
 
 def align_logits(logits: Sequence[Tensor], targets: Sequence[Tensor], *,
@@ -255,10 +268,11 @@ def align_logits(logits: Sequence[Tensor], targets: Sequence[Tensor], *,
         raise TypeError("check_inputs must be bool")
     if not (logits and isinstance(logits[0], Tensor) and logits[0].is_cuda):
         _metadata(logits, targets, blank_id)
-    load_extension()
+    if _native is None:
+        load_extension()
     tensors, lengths = _native.align(logits, targets, blank_id, mode == "optimized", check_inputs,
                                      emission_validity, True)
-    return AlignmentBatch(lengths, *tensors)
+    return _batch(lengths, tensors)
 
 
 def log_softmax(logits: Sequence[Tensor]) -> list[Tensor]:
