@@ -8,7 +8,8 @@ schema of alignment.cu:1065-1068.
   mixed batch against the CPU oracle with the same options, all ten outputs
   bit for bit.
 * A record of more than 512 chunks takes the tail kernel's global-memory slot
-  path (chunk_frames = 16, 9,000 frames).
+  path (chunk_frames = 16, 9,000 frames; chunk_frames = 32, 16,500 frames with
+  a saved frontier per chunk, counted in reuse_stats or not).
 """
 from __future__ import annotations
 
@@ -16,6 +17,7 @@ import numpy as np
 import pytest
 import torch
 
+import fast_forced_aligner as ffa
 import repair_cases as RC
 from fast_forced_aligner import workloads
 from helpers import FIELDS, assert_same
@@ -28,6 +30,7 @@ DEV = "cuda"
 def op_align(emissions, targets, blanks, knobs, check_inputs=True):
     """The reference-schema operator with an explicit knob vector; returns the
     ten outputs as numpy arrays plus lengths."""
+    ffa.load_extension()  # registers the fast_forced_aligner_cuda operators
     es = [torch.from_numpy(np.ascontiguousarray(e)).to(DEV) for e in emissions]
     ys = [torch.from_numpy(np.ascontiguousarray(y, dtype=np.int64)).to(DEV) for y in targets]
     k = knobs
@@ -182,3 +185,28 @@ def test_more_than_512_chunks_use_global_slots(knobs):
     assert got["repair_passes"][0] > 0 or got["routing_stats"][0, 0] == 2
     if knobs == dict(repair_budget_frames=0):
         assert got["repair_passes"][0] == 2 and got["stitched"][0] == 1
+
+
+@pytest.mark.parametrize("knobs", [dict(repair_budget_frames=0), dict(repair_budget_frames=0, frontier_min_frames=1 << 30)],
+                         ids=["counted", "uncounted"])
+def test_global_slots_resume_from_saved_frontiers(knobs):
+    """chunk_frames = 32 and 16,500 frames: 516 chunks in global-memory slots,
+    each with a saved frontier (every optimized-mode record keeps them at
+    chunk_frames >= 32). The repairs resume from them whether or not the
+    reference's reuse gating counts the record in reuse_stats."""
+    rng = np.random.default_rng(516)
+    T, V = 16500, 8
+    y = rng.integers(1, V, size=1200).astype(np.int64)
+    e = workloads.peaky(rng, y, T, V)
+    e[3000:3040] = rng.integers(-2, 1, (40, V)).astype(np.float32)
+    e[9000:9060] = workloads._log_softmax(2 * rng.standard_normal((60, V)).astype(np.float32))
+    k = RC.knob_vector(chunk_frames=32, **knobs)
+    print(f"global slots with frontiers {knobs}", flush=True)
+    got = op_align([e], [y], [0], k)
+    want = oracle_align([e], [y], [0], k)
+    assert_same(got, want, where="global-slot frontiers ")
+    assert got["repair_passes"][0] > 0
+    if "frontier_min_frames" in knobs:
+        assert got["reuse_stats"].shape == (0, 4)
+    else:
+        assert got["reuse_stats"][0, 0] > 0  # frames resumed by the repairs
