@@ -346,3 +346,34 @@ def test_state_widths_and_gathered_rows(mode, case):
     assert K == {"k16": 16, "gather_k4": 4, "gather_k8": 8}[case] and (S + K - 1) // K > 64  # several waves
     print(f"state widths {case} {mode}", flush=True)
     compare(es, ys, mode=mode, where=case)
+
+
+@pytest.mark.parametrize("mode", ["conventional", "optimized"])
+def test_vocabulary_and_length_limits(mode):
+    """The edges of the supported shapes in one ragged batch: a blank-only
+    vocabulary (V = 1, empty transcript), single-frame records, the blank in
+    the last column, the widest vocabulary (V = 8,192) with a peaky and a flat
+    record, and V = 65 / 64 on either side of the LDS emission blocks."""
+    rng = np.random.default_rng(8192)
+    es, ys, blanks = [], [], []
+
+    def add(e, y, blank):
+        es.append(np.ascontiguousarray(e, dtype=np.float32))
+        ys.append(np.asarray(y, dtype=np.int64))
+        blanks.append(blank)
+
+    add(workloads._log_softmax(rng.standard_normal((40, 1)).astype(np.float32)), [], 0)  # V = 1
+    add(workloads._log_softmax(rng.standard_normal((1, 5)).astype(np.float32)), [3], 0)  # T = 1
+    add(workloads._log_softmax(rng.standard_normal((1, 5)).astype(np.float32)), [], 4)   # T = 1, U = 0
+    y = rng.integers(0, 39, size=60)
+    add(workloads.peaky(rng, y, 300, 40, blank=39), y, 39)                              # blank = V - 1
+    y = rng.integers(1, 8192, size=90)
+    add(workloads.peaky(rng, y, 400, 8192), y, 0)                                       # V = 8192
+    add(workloads._log_softmax(0.1 * rng.standard_normal((150, 8192)).astype(np.float32)),
+        rng.integers(1, 8192, size=40), 0)
+    for V in (64, 65):
+        y = rng.integers(1, V, size=70)
+        add(workloads.peaky(rng, y, 260, V), y, 0)
+    print(f"shape limits {mode}", flush=True)
+    got = compare(es, ys, blank=blanks, mode=mode, where="limits")
+    assert (got["status"][[0, 1, 2, 3, 4, 6, 7]] == 0).all()
