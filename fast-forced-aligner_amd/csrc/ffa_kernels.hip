@@ -130,11 +130,13 @@ struct Params {
   Slot* slots;
   float* frontiers;
   int64_t budget, repair_min, frontier_min;
-  int32_t count, total_slots, H, mode, repair_rounds, check_inputs, overlap, frontier_batch;
+  int32_t count, total_slots, H, mode, repair_rounds, check_inputs, overlap;
+  int32_t tail_phase;  // TAIL_ALL, or a phase of the split tail (TAIL_PLAN0, TAIL_RESUME)
   int32_t u_cap, d_cap, v_words, lds_tail_slots;
   int32_t eblk_frames;  // frames per LDS emission block of the DP (0: rows read straight from HBM)
   int32_t logits;       // emissions are raw logits, aligned as their row log-softmax
   float2* stats;        // logits: per frame {row max, log of the row's exp-sum}, indexed like labels
+  struct TailState* tstate;  // split tail: per-record state between its phases
 };
 
 // ---------------------------------------------------------------------------
@@ -148,6 +150,25 @@ struct TailStats {
   int64_t repaired;                              // repaired_frames
   int early, rejected, maxprop, passes;          // routing_stats, repair_passes
 };
+
+// The record's tail state in global memory for the split tail (batches with
+// records of at least 2,048 frames): the tail kernel plans the first repair
+// round (TAIL_PLAN0), repair_kernel runs that round's DPs with one workgroup
+// per merged interval (alignment.cu:727-760 gives each interval its own CTA
+// the same way) or the early full fallback, and the record's last workgroup
+// to finish runs the later rounds and the seam check (TAIL_RESUME).
+struct TailState {
+  TailStats ts;
+  int32_t done;     // the record's outputs are written (rejected, or stitched on the fast path)
+  int32_t status;   // after an early full fallback
+  float objective;  // after an early full fallback
+  int32_t work;     // first-round DPs planned for the record (repair intervals or the early fallback)
+  int32_t pending;  // of those, not finished yet
+  int32_t pad[3];
+};
+static_assert(sizeof(TailState) % 16 == 0, "16-byte granules");
+
+enum { TAIL_ALL = 0, TAIL_PLAN0 = 1, TAIL_RESUME = 2 };
 
 struct StageWave {  // one wave's target staging summary (chunk kernel)
   int flags;      // 1 out-of-vocabulary id, 2 blank id among the targets
@@ -1947,15 +1968,22 @@ __device__ __attribute__((always_inline)) DPOut run_dp(const Params& p, const Re
 }
 
 // The tail of one record; SP is the slot array, in LDS or in global memory.
+// With phase TAIL_ALL it runs every repair round's DPs itself, one interval
+// after another. In the split tail, TAIL_PLAN0 plans the first round and
+// leaves its DPs to repair_kernel; TAIL_RESUME (in repair_kernel, once the
+// record's first-round DPs are done) runs the later rounds and the seam check.
+// The record's state lives in p.tstate between the two.
 template <int K, int D, bool LG, class SP>
 __device__ __attribute__((always_inline)) void tail_body(const Params& p, const RecordDesc& d, int rec, const Rec& r,
-                                                      const Lds& L, SP sl, bool in_lds) {
+                                                      const Lds& L, SP sl, bool in_lds, int phase) {
   Header* h = L.h;
   const int tid = threadIdx.x;
   const int64_t T = r.T;
   const int n = (int)(1 + (T - 1) / p.H);
+  const bool split = phase != TAIL_ALL;
+  GLB TailState* state = split ? glb(p.tstate) + rec : nullptr;
   const int status0 = sl[0].status;
-  if (status0 >= 2) {
+  if (status0 >= 2 && (!split || phase == TAIL_PLAN0)) {
     if (tid == 0) {
       glb(p.status)[rec] = status0;
       glb(p.objective)[rec] = NEG_INF;
@@ -1965,6 +1993,7 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
       for (int q = 0; q < 3; ++q) { glb(p.shortcut_stats)[3 * rec + q] = 0; glb(p.routing_stats)[3 * rec + q] = 0; }
       if (p.reuse_stats)
         for (int q = 0; q < 4; ++q) glb(p.reuse_stats)[4 * rec + q] = 0;
+      if (split) state->done = 1;
     }
     return;
   }
@@ -1977,7 +2006,7 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
   // nothing (plan_repairs joins every neighbour and its budget preflight
   // proposes no region) and validate_seams stitches iff the fp32 total is
   // finite. Wave 0 checks all seams at once and writes the result.
-  if (n <= 64 && in_lds) {
+  if (n <= 64 && in_lds && (!split || phase == TAIL_PLAN0)) {
     if (tid < 64) {
       const int k = tid;
       const bool valid = k < n;
@@ -2010,6 +2039,7 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
               GLB int64_t* u = glb(p.reuse_stats) + 4 * rec;
               u[0] = 0; u[1] = 0; u[2] = counted ? (int64_t)__popcll(dp) * S : 0; u[3] = 0;
             }
+            if (split) state->done = 1;
           }
         }
       }
@@ -2020,21 +2050,37 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
     __syncthreads();
   }
   TailStats& ts = h->ts;  // written by thread 0 only
-  if (tid == 0) {  // shortcut_stats (cu:129-133, 140-146) and frontier writes of the chunk DPs
-    ts = TailStats{};
-    for (int k = 0; k < n; ++k) {
-      if (sl[k].kind == 1) { ++ts.sc_accepted; ts.sc_frames += sl[k].b - sl[k].a; }
-      else {
-        if (sl[k].kind == 2) ++ts.sc_ambiguous;
-        if (counted) ts.reuse[2] += S;
-      }
-    }
-  }
   int early = 0;  // uniform copy of ts.early
   int status = 0;
   float objective = NEG_INF;
+  if (!split || phase == TAIL_PLAN0) {
+    if (tid == 0) {  // shortcut_stats (cu:129-133, 140-146) and frontier writes of the chunk DPs
+      ts = TailStats{};
+      for (int k = 0; k < n; ++k) {
+        if (sl[k].kind == 1) { ++ts.sc_accepted; ts.sc_frames += sl[k].b - sl[k].a; }
+        else {
+          if (sl[k].kind == 2) ++ts.sc_ambiguous;
+          if (counted) ts.reuse[2] += S;
+        }
+      }
+    }
+  } else {  // a later phase: the state the previous phases left
+    if (tid == 0) {
+      ts = load_pod(&state->ts);
+      h->ibuf[5] = ts.early;
+      h->ibuf[7] = state->status;
+      h->fbuf[3] = state->objective;
+    }
+    __syncthreads();
+    early = h->ibuf[5];
+    status = h->ibuf[7];
+    objective = h->fbuf[3];
+    __syncthreads();
+  }
   const bool repairs = p.repair_rounds > 0;
-  for (int round = 0; round < p.repair_rounds; ++round) {
+  const int first_round = phase == TAIL_RESUME ? 1 : 0;
+  const int end_round = phase == TAIL_PLAN0 ? 1 : p.repair_rounds;
+  for (int round = first_round; round < end_round; ++round) {
     if (tid == 0) {  // plan_repairs, cu:164-228
       early = ts.early;
       int run = !(p.overlap && early == 2);
@@ -2090,6 +2136,7 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
     __syncthreads();
     early = h->ibuf[5];
     __syncthreads();
+    if (phase == TAIL_PLAN0) break;  // the first round's DPs run in repair_kernel
     if (p.overlap && early) {
       if (early == 1) {  // early full fallback (repair_recurrence, cu:535-550)
         const Slot s0 = load_slot(sl + (0));
@@ -2129,6 +2176,24 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
         __syncthreads();
       }
     }
+  }
+  if (phase == TAIL_PLAN0) {  // hand the planned round to repair_kernel
+    if (in_lds) {
+      GLB Slot* gs = glb(p.slots) + d.chunk_offset;
+      for (int k = tid; k < n; k += blockDim.x) store_pod(gs + k, load_slot(sl + k));
+    }
+    if (tid == 0) {
+      int work = p.overlap && early == 1 ? 1 : 0;  // the early full fallback
+      if (!(p.overlap && early))
+        for (int k = 0; k < n; ++k) work += sl[k].a < sl[k].b && sl[k].flag;
+      store_pod(&state->ts, ts);
+      state->done = 0;
+      state->status = 0;
+      state->objective = NEG_INF;
+      state->work = work;
+      state->pending = work;
+    }
+    return;
   }
   int stitched = 0;
   if (!(p.overlap && early == 2)) {  // validate_seams, cu:562-592
@@ -2367,6 +2432,7 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) tail_kernel(Params p) {
   const RecordDesc d = load_uniform(p.desc + rec);
   const int n = (int)(1 + (d.frames - 1) / p.H);
   GLB Slot* gs = glb(p.slots) + d.chunk_offset;
+  const bool split = p.tail_phase != TAIL_ALL;
   if (n <= 64) {
     if (tid < 64) {
       const int k = tid;
@@ -2424,6 +2490,7 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) tail_kernel(Params p) {
           }
         }
       }
+      if (split && done && k == 0) glb(p.tstate)[rec].done = 1;
       if (tid == 0) h->last = done;
     }
     __syncthreads();
@@ -2436,9 +2503,107 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) tail_kernel(Params p) {
     Slot* ls = reinterpret_cast<Slot*>(lds_raw + ((uintptr_t)L.tslots - (uintptr_t)lds_raw));
     for (int k = tid; k < n; k += blockDim.x) ls[k] = load_pod(gs + k);
     __syncthreads();
-    tail_body<K, D, LG>(p, d, rec, r, L, ls, true);
+    tail_body<K, D, LG>(p, d, rec, r, L, ls, true, p.tail_phase);
   } else {
-    tail_body<K, D, LG>(p, d, rec, r, L, gs, false);
+    tail_body<K, D, LG>(p, d, rec, r, L, gs, false, p.tail_phase);
+  }
+}
+
+// Split tail, after TAIL_PLAN0: one workgroup per (chunk k, record) runs the
+// first round's repair DP of the merged interval that starts at chunk k
+// (repair DP over merged intervals, cu:727-760), or, in chunk 0's workgroup,
+// the record's early full fallback (repair_recurrence, cu:535-550). The
+// record's reuse_stats counters are added atomically; each workgroup writes
+// only its own slot. The record's last workgroup to finish (an arrival count
+// behind an agent-scope release, so its slots and labels are visible to
+// whichever workgroup continues, on any XCD) then runs the later rounds and
+// the seam check for the record; a record with no first-round DP continues in
+// chunk 0's workgroup. Records therefore progress independently: a long
+// fallback in one record delays no other record's later rounds.
+template <int K, int D, bool LG>
+__global__ void __launch_bounds__(K == 32 ? 640 : 256) repair_kernel(Params p) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  const Lds L = carve(lds_raw, p);
+  Header* h = L.h;
+  const int tid = threadIdx.x;
+  const int k = blockIdx.x, rec = blockIdx.y;
+  const RecordDesc d = load_uniform(p.desc + rec);
+  const int n = (int)(1 + (d.frames - 1) / p.H);
+  if (k >= n) return;
+  GLB TailState* state = glb(p.tstate) + rec;
+  if (__builtin_amdgcn_readfirstlane(state->done)) return;
+  const int early = __builtin_amdgcn_readfirstlane(state->ts.early);  // 0 or 1 as planned (the fallback writes 2)
+  const int work = __builtin_amdgcn_readfirstlane(state->work);
+  GLB Slot* slot = glb(p.slots) + d.chunk_offset + k;
+  const Slot s = load_uniform(p.slots + d.chunk_offset + k);
+  const bool fallback = p.overlap && early == 1 && k == 0;
+  const bool repair = !(p.overlap && early) && s.a < s.b && s.flag;
+  if (!fallback && !repair && !(work == 0 && k == 0)) return;
+  Rec r = make_rec(d, p, L);
+  if (LG) r.st = p.stats + d.frame_offset;
+  load_tokens(r, L.ytok);
+  const int64_t T = r.T;
+  const int S = r.S;
+  const bool frontier_on = r.frontier != nullptr;
+  const bool counted = frontier_on && (d.flags & DESC_REUSE_COUNTED);
+  unsigned long long* reuse = reinterpret_cast<unsigned long long*>(p.tstate[rec].ts.reuse);
+  if (fallback) {
+    const bool resume = frontier_on && s.frontier_end > 0 && s.frontier_end <= T;
+    if (resume && counted && tid == 0) {
+      atomicAdd(reuse + 1, (unsigned long long)s.frontier_end);
+      atomicAdd(reuse + 3, (unsigned long long)S);
+    }
+    const DPOut o = run_dp<K, D, LG>(p, r, L, 0, T, true, resume ? r.frontier : nullptr,
+                                     resume ? s.frontier_end : 1, nullptr, TRACE_IF_FINITE);
+    if (tid == 0) {
+      state->status = isfinite(o.score) ? 0 : 1;
+      state->objective = o.score;
+      state->ts.early = 2;
+    }
+  } else if (repair) {
+    bool resume = false;
+    int64_t start_t = s.a + 1;
+    GLB float* fr = frontier_on ? r.frontier + (int64_t)k * S : nullptr;
+    if (frontier_on) {
+      if (s.frontier_end > s.a && s.frontier_end <= s.b) {
+        resume = true;
+        start_t = s.frontier_end;
+        if (tid == 0 && counted) {
+          atomicAdd(reuse + 0, (unsigned long long)(s.frontier_end - s.a));
+          atomicAdd(reuse + 3, (unsigned long long)S);
+        }
+      }
+      if (tid == 0 && counted) atomicAdd(reuse + 2, (unsigned long long)S);
+    }
+    const DPOut o = run_dp<K, D, LG>(p, r, L, s.a, s.b, s.b == T, resume ? fr : nullptr, start_t, fr, TRACE_ALWAYS);
+    if (tid == 0) {
+      Slot out = s;
+      out.objective = o.score;
+      out.end = o.terminal;
+      out.start = o.start;
+      if (frontier_on) out.frontier_end = s.b;
+      store_pod(slot, out);
+    }
+  }
+  if (work > 0) {
+    // every thread's writes (slot, labels, scores, state) reach the device
+    // before the arrival is counted; the last arrival continues the record
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) h->last = __hip_atomic_fetch_sub(&p.tstate[rec].pending, 1, __ATOMIC_ACQ_REL,
+                                                   __HIP_MEMORY_SCOPE_AGENT) == 1;
+    __syncthreads();
+    if (!h->last) return;
+    __threadfence();
+  }
+  GLB Slot* gs = glb(p.slots) + d.chunk_offset;
+  if (n <= p.lds_tail_slots) {
+    Slot* ls = reinterpret_cast<Slot*>(lds_raw + ((uintptr_t)L.tslots - (uintptr_t)lds_raw));
+    for (int j = tid; j < n; j += blockDim.x) ls[j] = load_pod(gs + j);
+    __syncthreads();
+    tail_body<K, D, LG>(p, d, rec, r, L, ls, true, TAIL_RESUME);
+  } else {
+    tail_body<K, D, LG>(p, d, rec, r, L, gs, false, TAIL_RESUME);
   }
 }
 
@@ -2592,12 +2757,13 @@ inline int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 enum {
   I_K, I_NT, I_SLOTS, I_LDS, I_UCAP, I_DCAP, I_VWORDS, I_TAILSLOTS, I_FRONTIER, I_BUDGET,
   I_OVERLAP, I_WS_SLOTS, I_WS_FRONTIER, I_MODE, I_H, I_FMIN, I_REPAIR_MIN, I_EBLK, I_LOGITS, I_WS_STATS,
-  I_MAX_FRAMES, I_WS_BP
+  I_MAX_FRAMES, I_WS_BP, I_SPLIT, I_WS_TSTATE
 };
+static_assert(I_WS_TSTATE < 24, "plan->internal holds 24 values");
 
 template <int K, int D, bool LG, class TB>
-int launch_geometry(const ffa::Params& p, const TB& tab, int NT, size_t lds, bool optimized, int64_t max_frames,
-                    hipStream_t stream) {
+int launch_geometry(const ffa::Params& p, const TB& tab, int NT, size_t lds, bool optimized, bool split,
+                    int64_t max_frames, hipStream_t stream) {
   hipEvent_t start = g_profile_start, stop = g_profile_stop;
   g_profile_start = g_profile_stop = nullptr;
   if (p.logits && !optimized)
@@ -2611,7 +2777,16 @@ int launch_geometry(const ffa::Params& p, const TB& tab, int NT, size_t lds, boo
     hipLaunchKernelGGL((ffa::chunk_kernel<K, D, LG, TB>), dim3(grid), dim3(std::max(NT, 128)), lds, stream, p, tab);
   }
   if (stop) (void)hipEventRecord(stop, stream);
-  if (optimized) hipLaunchKernelGGL((ffa::tail_kernel<K, D, LG>), dim3(p.count), dim3(NT), lds, stream, p);
+  if (optimized && split) {  // first-round planning, then one workgroup per first-round interval
+    ffa::Params q = p;
+    const int64_t n_max = 1 + (max_frames - 1) / p.H;
+    q.tail_phase = ffa::TAIL_PLAN0;
+    hipLaunchKernelGGL((ffa::tail_kernel<K, D, LG>), dim3(p.count), dim3(NT), lds, stream, q);
+    hipLaunchKernelGGL((ffa::repair_kernel<K, D, LG>), dim3((unsigned)n_max, (unsigned)p.count), dim3(NT), lds, stream,
+                       q);
+  } else if (optimized) {
+    hipLaunchKernelGGL((ffa::tail_kernel<K, D, LG>), dim3(p.count), dim3(NT), lds, stream, p);
+  }
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(FFA_E_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
   return FFA_OK;
@@ -2774,6 +2949,12 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
   ws += align_up(32 * slots, 256);
   const int64_t ws_frontier = ws;
   ws += align_up(4 * frontier_floats, 256);
+  // split tail: batches with a record of at least 2,048 frames run each repair
+  // round's intervals in parallel workgroups (a few more launches, against
+  // repair DPs of milliseconds)
+  const bool split = optimized && o->repair_rounds > 0 && max_frames >= 2048 && count * n_max <= (1 << 20);
+  const int64_t ws_tstate = ws;
+  if (split) ws += align_up((int64_t)sizeof(ffa::TailState) * count, 256);
   const int64_t ws_stats = ws;
   if (logits) ws += align_up(8 * total_frames, 256);
   std::memset(plan, 0, sizeof(*plan));
@@ -2806,6 +2987,8 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
   in[I_WS_STATS] = ws_stats;
   in[I_MAX_FRAMES] = max_frames;
   in[I_WS_BP] = ws_bp;
+  in[I_SPLIT] = split ? 1 : 0;
+  in[I_WS_TSTATE] = ws_tstate;
   return FFA_OK;
 }
 
@@ -2908,7 +3091,6 @@ extern "C" int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_opti
   p.repair_rounds = (int32_t)o->repair_rounds;
   p.check_inputs = o->check_inputs ? 1 : 0;
   p.overlap = (int32_t)in[I_OVERLAP];
-  p.frontier_batch = (int32_t)in[I_FRONTIER];
   p.u_cap = (int32_t)in[I_UCAP];
   p.d_cap = (int32_t)in[I_DCAP];
   p.v_words = (int32_t)in[I_VWORDS];
@@ -2919,17 +3101,19 @@ extern "C" int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_opti
   const int NT = (int)in[I_NT];
   const size_t lds = (size_t)in[I_LDS];
   const int64_t max_frames = in[I_MAX_FRAMES];
+  const bool split = in[I_SPLIT] != 0;
+  p.tstate = split ? reinterpret_cast<ffa::TailState*>(ws + in[I_WS_TSTATE]) : nullptr;
   auto run = [&](const auto& tab) -> int {
     using TB = std::decay_t<decltype(tab)>;
     switch (in[I_K]) {
-      case 4: return p.logits ? launch_geometry<4, 8, true, TB>(p, tab, NT, lds, optimized, max_frames, stream)
-                              : launch_geometry<4, 8, false, TB>(p, tab, NT, lds, optimized, max_frames, stream);
-      case 8: return p.logits ? launch_geometry<8, 6, true, TB>(p, tab, NT, lds, optimized, max_frames, stream)
-                              : launch_geometry<8, 6, false, TB>(p, tab, NT, lds, optimized, max_frames, stream);
-      case 16: return p.logits ? launch_geometry<16, 4, true, TB>(p, tab, NT, lds, optimized, max_frames, stream)
-                               : launch_geometry<16, 4, false, TB>(p, tab, NT, lds, optimized, max_frames, stream);
-      case 32: return p.logits ? launch_geometry<32, 1, true, TB>(p, tab, NT, lds, optimized, max_frames, stream)
-                               : launch_geometry<32, 1, false, TB>(p, tab, NT, lds, optimized, max_frames, stream);
+      case 4: return p.logits ? launch_geometry<4, 8, true, TB>(p, tab, NT, lds, optimized, split, max_frames, stream)
+                              : launch_geometry<4, 8, false, TB>(p, tab, NT, lds, optimized, split, max_frames, stream);
+      case 8: return p.logits ? launch_geometry<8, 6, true, TB>(p, tab, NT, lds, optimized, split, max_frames, stream)
+                              : launch_geometry<8, 6, false, TB>(p, tab, NT, lds, optimized, split, max_frames, stream);
+      case 16: return p.logits ? launch_geometry<16, 4, true, TB>(p, tab, NT, lds, optimized, split, max_frames, stream)
+                               : launch_geometry<16, 4, false, TB>(p, tab, NT, lds, optimized, split, max_frames, stream);
+      case 32: return p.logits ? launch_geometry<32, 1, true, TB>(p, tab, NT, lds, optimized, split, max_frames, stream)
+                               : launch_geometry<32, 1, false, TB>(p, tab, NT, lds, optimized, split, max_frames, stream);
       default: return fail(FFA_E_INVALID, "corrupt plan");
     }
   };
