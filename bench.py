@@ -450,6 +450,13 @@ def main() -> int:
         return step_s, kernel_ms, achieved, result
 
     kernel_name = "chunk_kernel" if args.mode == "optimized" else "conventional_kernel"
+    # optimized mode runs each record's tail inside the chunk kernel (one launch
+    # per call) for batches of log-probabilities with at most 1,024 chunks, at
+    # most 4,096 states and no record of 2,048+ frames (the split tail's
+    # batches); otherwise a tail kernel follows (align_launch, ffa_kernels.hip)
+    chunks = sum((e.shape[0] + 127) // 128 for e in batch.emissions)
+    fused_tail = (args.mode == "optimized" and chunks <= 1024 and max(e.shape[0] for e in batch.emissions) < 2048
+                  and max(2 * len(y) + 1 for y in batch.targets) <= 4096)
     step_s, kernel_ms, achieved, result = figures(args.mode, args.steps, args.warmup)
     # parity spot check outside the timed region
     from oracle import oracle
@@ -480,6 +487,8 @@ def main() -> int:
                      "traffic": measured_traffic(args.config, args.mode, kernel_name),
                      "kernel": kernel_name, "kernel_us": kernel_ms * 1e3, "algorithmic_bytes": min_bytes},
     }
+    if args.mode == "optimized":
+        line["roofline"]["tail"] = "fused" if fused_tail else "tail_kernel"
     # the same timing of an empty kernel with the dominant kernel's workgroup
     # count, and the fraction a kernel of exactly that duration would reach
     groups = 8 * ((sum((e.shape[0] + 127) // 128 for e in batch.emissions) + 7) // 8) \

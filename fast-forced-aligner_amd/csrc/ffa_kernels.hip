@@ -33,9 +33,11 @@
 #include <cstdio>
 #include <cstring>
 #include <algorithm>
+#include <map>
 #include <mutex>
 #include <string>
 #include <type_traits>
+#include <utility>
 #include <vector>
 
 #include "ffa.h"
@@ -137,6 +139,7 @@ struct Params {
   int32_t logits;       // emissions are raw logits, aligned as their row log-softmax
   float2* stats;        // logits: per frame {row max, log of the row's exp-sum}, indexed like labels
   struct TailState* tstate;  // split tail: per-record state between its phases
+  int32_t* arrivals;         // fused tail: per-record count of finished chunks, zero between calls
 };
 
 // ---------------------------------------------------------------------------
@@ -196,6 +199,7 @@ struct Header {
   };
   int gbad[2];         // per-wave greedy rejection (fast path)
   int last;            // the record's outputs are written (tail fast path)
+  int arrived;         // fused tail: this workgroup is the record's last chunk to finish
   TailStats ts;
 };
 
@@ -303,6 +307,38 @@ __device__ inline void store_pod(GLB T* dst, const T& value) {
 #pragma unroll
   for (size_t i = 0; i < sizeof(T) / 16; ++i) ((GLB v4i_t*)dst)[i] = tmp[i];
 }
+// Agent-scope (relaxed atomic) stores and loads: the store is written through
+// this XCD's L2, the load is served past it, so workgroups on other XCDs of the
+// same kernel see the value without an L2 write-back or invalidation. With AG
+// false they are ordinary accesses.
+template <bool AG, class T>
+__device__ inline void put(GLB T* dst, T value) {
+  if constexpr (AG) __hip_atomic_store((T*)dst, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else *dst = value;
+}
+template <class T>
+__device__ inline void store_pod_agent(GLB T* dst, const T& value) {
+  static_assert(sizeof(T) % 8 == 0, "8-byte words");
+  uint64_t tmp[sizeof(T) / 8];
+  __builtin_memcpy(tmp, &value, sizeof(T));
+#pragma unroll
+  for (size_t i = 0; i < sizeof(T) / 8; ++i)
+    __hip_atomic_store((uint64_t*)dst + i, tmp[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ inline T load_pod_agent(const GLB T* src) {
+  static_assert(sizeof(T) % 8 == 0, "8-byte words");
+  uint64_t tmp[sizeof(T) / 8];
+#pragma unroll
+  for (size_t i = 0; i < sizeof(T) / 8; ++i)
+    tmp[i] = __hip_atomic_load((const uint64_t*)src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  T out;
+  __builtin_memcpy(&out, tmp, sizeof(T));
+  return out;
+}
+// Waits until every earlier global store of this wave is complete (for
+// agent-scope stores: visible to the whole GPU).
+__device__ inline void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 
 // ---------------------------------------------------------------------------
@@ -1433,6 +1469,8 @@ __device__ __attribute__((always_inline)) int place_literal(const Lds& L, const 
 // *ambiguous is set when more than one placement is legal.
 constexpr int CAND_CAP = 256;
 
+// AG: labels and scores are written with agent-scope stores (fused tail).
+template <bool AG>
 __device__ __attribute__((always_inline)) int greedy_chunk(const Rec& r, const Lds& L, int64_t a, int64_t b, bool blank_in, Slot& out, int* ambiguous) {
   Header* h = L.h;
   const int tid = threadIdx.x, NT = blockDim.x;
@@ -1593,8 +1631,8 @@ __device__ __attribute__((always_inline)) int greedy_chunk(const Rec& r, const L
   const float score = h->fbuf[1];
   if (!isfinite(score)) { __syncthreads(); return 0; }  // cu:139
   for (int f = tid; f < n; f += NT) {  // finish's label/score gather collapses to g and fs here
-    r.labels[a + f] = L.g[f];
-    r.scores[a + f] = L.fs[f];
+    put<AG>(r.labels + a + f, (int64_t)L.g[f]);
+    put<AG>(r.scores + a + f, (float)L.fs[f]);
   }
   out.start = start;
   out.end = start + rlast;
@@ -2249,11 +2287,108 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
   }
 }
 
+// Fast path of one record's tail in wave 0 (tid < 64, n <= 64 chunks): a
+// rejected record, or every seam legal and a finite total, writes the record's
+// outputs. Returns 1 when the record is finished. AG: the slots are read with
+// agent-scope loads (fused tail: written by workgroups of the same kernel).
+template <bool AG>
+__device__ __attribute__((always_inline)) int tail_fast(const Params& p, const RecordDesc& d, int rec, const GLB Slot* gs,
+                                                        int n) {
+  const int k = threadIdx.x;
+  const bool valid = k < n;
+  const Slot sk = AG ? load_pod_agent(gs + (valid ? k : 0)) : load_pod(gs + (valid ? k : 0));
+  const int status0 = __builtin_amdgcn_readfirstlane(sk.status);
+  const int S = 2 * d.tokens + 1;
+  const bool counted = d.frontier_offset >= 0 && (d.flags & DESC_REUSE_COUNTED);
+  int done = 0;
+  if (status0 >= 2) {  // rejected record: every chunk wrote -1 / -inf
+    done = 1;
+    if (k == 0) {
+      glb(p.status)[rec] = status0;
+      glb(p.objective)[rec] = NEG_INF;
+      glb(p.stitched)[rec] = 0;
+      glb(p.repair_passes)[rec] = 0;
+      glb(p.repaired_frames)[rec] = 0;
+      for (int q = 0; q < 3; ++q) { glb(p.shortcut_stats)[3 * rec + q] = 0; glb(p.routing_stats)[3 * rec + q] = 0; }
+      if (p.reuse_stats)
+        for (int q = 0; q < 4; ++q) glb(p.reuse_stats)[4 * rec + q] = 0;
+    }
+  } else {
+    const int end_prev = wave_shr1_int(sk.end, 0);
+    bool ok = !valid || isfinite(sk.objective);
+    if (valid && k > 0) {  // legal_seam, cu:157-161
+      const int jump = sk.start - end_prev;
+      ok = ok && (jump == 0 || jump == 1 || (jump == 2 && sk.skip_ok));
+    }
+    if (__ballot(!ok) == 0) {
+      float total = 0.0f;  // cu:578-584: chunk objectives summed in chunk order
+      for (int i = 0; i < n; ++i) total += readlane_f(sk.objective, i);
+      if (isfinite(total)) {
+        done = 1;
+        const uint64_t shortcut = __ballot(valid && sk.kind == 1);
+        const uint64_t amb = __ballot(valid && sk.kind == 2);
+        const uint64_t dp = __ballot(valid && sk.kind != 1);
+        int frames = valid && sk.kind == 1 ? sk.b - sk.a : 0;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) frames += __shfl_xor(frames, off, 64);
+        if (k == 0) {
+          glb(p.status)[rec] = 0;
+          glb(p.objective)[rec] = total;
+          glb(p.stitched)[rec] = 1;
+          glb(p.repair_passes)[rec] = 0;
+          glb(p.repaired_frames)[rec] = 0;
+          glb(p.shortcut_stats)[3 * rec + 0] = __popcll(shortcut);
+          glb(p.shortcut_stats)[3 * rec + 1] = frames;
+          glb(p.shortcut_stats)[3 * rec + 2] = __popcll(amb);
+          for (int q = 0; q < 3; ++q) glb(p.routing_stats)[3 * rec + q] = 0;
+          if (p.reuse_stats) {
+            GLB int64_t* u = glb(p.reuse_stats) + 4 * rec;
+            u[0] = 0; u[1] = 0; u[2] = counted ? (int64_t)__popcll(dp) * S : 0; u[3] = 0;
+          }
+        }
+      }
+    }
+  }
+  return done;
+}
+
+// The rest of one record's tail (every thread of the workgroup): its slots
+// into LDS when they fit, then tail_body.
+template <int K, int D, bool LG>
+__device__ __attribute__((always_inline)) void tail_rest(const Params& p, const RecordDesc& d, int rec, const Lds& L,
+                                                         int phase) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  const int tid = threadIdx.x;
+  const int n = (int)(1 + (d.frames - 1) / p.H);
+  GLB Slot* gs = glb(p.slots) + d.chunk_offset;
+  Rec r = make_rec(d, p, L);
+  if (LG) r.st = p.stats + d.frame_offset;
+  if (n <= p.lds_tail_slots) {
+    Slot* ls = reinterpret_cast<Slot*>(lds_raw + ((uintptr_t)L.tslots - (uintptr_t)lds_raw));
+    for (int k = tid; k < n; k += blockDim.x) ls[k] = load_pod(gs + k);
+    __syncthreads();
+    tail_body<K, D, LG>(p, d, rec, r, L, ls, true, phase);
+  } else {
+    tail_body<K, D, LG>(p, d, rec, r, L, gs, false, phase);
+  }
+}
+
 // Optimized mode, one workgroup per chunk of H frames (XCD-aware order): it
 // stages and validates the record's targets, takes the greedy shortcut
 // (cu:30-153) or runs the relaxed chunk DP (cu:721-726), and writes the
 // chunk's labels, scores and slot.
-template <int K, int D, bool LG, class TB>
+//
+// FUSE (fused tail): the record's last chunk workgroup to finish, on whichever
+// XCD it runs, then runs the record's tail (tail_kernel's work) itself, so a
+// call needs one launch. Hand-off: a chunk that took the greedy shortcut (or
+// was rejected) writes its labels, scores and slot with agent-scope stores
+// and waits for their completion; a chunk that ran a DP wrote backpointers,
+// frontiers and its path with ordinary stores and releases them at agent
+// scope (an L2 write-back, which only the rarer DP chunks pay). Then one
+// arrival on the record's counter; the last one zeroes it for the next call.
+// The tail's fast path reads the slots with agent-scope loads; the full tail
+// first acquires at agent scope.
+template <int K, int D, bool LG, class TB, bool FUSE>
 __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p, TB tab) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   const Lds L = carve(lds_raw, p);
@@ -2338,7 +2473,7 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p, TB
   }
   // the tail kernel reads the record's descriptor from the workspace (stored
   // after the row loads are issued, so the waits for the targets do not count it)
-  if constexpr (kArgs<TB>)
+  if constexpr (kArgs<TB> && !FUSE)
     if (chunk == 0 && tid == 0) store_pod(glb(const_cast<RecordDesc*>(p.desc)) + rec, d);
   const Staged st = fast ? finish_targets<ALPHABET_MASK32, true, true>(tl, d.vocab, d.blank, d.frames, rec, p, L)
                    : p.mode == 2 ? finish_targets<ALPHABET_BITMAP, false, true>(tl, d.vocab, d.blank, d.frames, rec, p, L)
@@ -2366,6 +2501,7 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p, TB
     }
   }
   Slot out{};
+  bool ran_dp = false;
   out.a = (int)a;
   out.b = (int)b;
   out.flag = 1;
@@ -2373,7 +2509,7 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p, TB
   GLB int64_t* labels = glb(p.labels) + d.frame_offset + a;
   GLB float* scores = glb(p.scores) + d.frame_offset + a;
   if (st.status >= 2) {  // rejected before any label-indexed read (cu:36, cu:642-652)
-    for (int f = tid; f < n; f += blockDim.x) { labels[f] = -1; scores[f] = NEG_INF; }
+    for (int f = tid; f < n; f += blockDim.x) { put<FUSE>(labels + f, (int64_t)-1); put<FUSE>(scores + f, NEG_INF); }
     out.flag = 0;
     out.status = (int16_t)st.status;
   } else {
@@ -2384,15 +2520,16 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p, TB
       accepted = greedy_fast(L, x, whole, n, d.tokens, 2 * d.tokens + 1, d.vocab, d.blank, st.alpha32, st.blank_in,
                              a == 0, b == d.frames, out, &ambiguous, &g, &fs);
       if (accepted && tid < n) {  // finish's label/score gather collapses to g and fs (cu:642-667)
-        labels[tid] = g;
-        scores[tid] = fs;
+        put<FUSE>(labels + tid, (int64_t)g);
+        put<FUSE>(scores + tid, fs);
       }
     }
     if (!accepted) {
       Rec r = make_rec(d, p, L);
       if (LG) { r.st = L.st; r.st_first = a; }
-      if (p.mode == 2 && !fast) accepted = greedy_chunk(r, L, a, b, st.blank_in, out, &ambiguous);
+      if (p.mode == 2 && !fast) accepted = greedy_chunk<FUSE>(r, L, a, b, st.blank_in, out, &ambiguous);
       if (!accepted) {  // initial chunk DP (cu:721-726), relaxed init for a > 0
+        ran_dp = true;
         GLB float* fr = r.frontier ? r.frontier + chunk * r.S : nullptr;
         const DPOut o = run_dp<K, D, LG>(p, r, L, a, b, b == r.T, nullptr, a + 1, fr, TRACE_ALWAYS);
         out.objective = o.score;
@@ -2409,7 +2546,36 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p, TB
       out.skip_ok = (int16_t)(l0 != d.blank && l0 != l2);
     }
   }
-  if (tid == 0) store_pod(glb(p.slots) + slot_index, out);
+  if constexpr (!FUSE) {
+    if (tid == 0) store_pod(glb(p.slots) + slot_index, out);
+  } else {
+    Header* h = L.h;
+    const int chunks = (int)(1 + (d.frames - 1) / p.H);
+    if (tid == 0) store_pod_agent(glb(p.slots) + slot_index, out);
+    if (ran_dp) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    else wait_stores();
+    __syncthreads();
+    if (tid == 0) {
+      const int old = ran_dp ? __hip_atomic_fetch_add(p.arrivals + rec, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT)
+                             : __hip_atomic_fetch_add(p.arrivals + rec, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = old == chunks - 1;
+      if (last) __hip_atomic_store(p.arrivals + rec, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      h->arrived = last;
+    }
+    __syncthreads();
+    if (!h->arrived) return;
+    if (chunks <= 64) {
+      if (tid < 64) {
+        const int done = tail_fast<true>(p, d, rec, glb(p.slots) + d.chunk_offset, chunks);
+        if (tid == 0) h->last = done;
+      }
+      __syncthreads();
+      if (h->last) return;
+      __syncthreads();
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    tail_rest<K, D, LG>(p, d, rec, L, TAIL_ALL);
+  }
 }
 
 // Optimized mode, one workgroup per record, after the chunk kernel: repair
@@ -2431,82 +2597,18 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) tail_kernel(Params p) {
   const int rec = blockIdx.x;
   const RecordDesc d = load_uniform(p.desc + rec);
   const int n = (int)(1 + (d.frames - 1) / p.H);
-  GLB Slot* gs = glb(p.slots) + d.chunk_offset;
   const bool split = p.tail_phase != TAIL_ALL;
   if (n <= 64) {
     if (tid < 64) {
-      const int k = tid;
-      const bool valid = k < n;
-      const Slot sk = load_pod(gs + (valid ? k : 0));
-      const int status0 = __builtin_amdgcn_readfirstlane(sk.status);
-      const int S = 2 * d.tokens + 1;
-      const bool counted = d.frontier_offset >= 0 && (d.flags & DESC_REUSE_COUNTED);
-      int done = 0;
-      if (status0 >= 2) {  // rejected record: every chunk wrote -1 / -inf
-        done = 1;
-        if (k == 0) {
-          glb(p.status)[rec] = status0;
-          glb(p.objective)[rec] = NEG_INF;
-          glb(p.stitched)[rec] = 0;
-          glb(p.repair_passes)[rec] = 0;
-          glb(p.repaired_frames)[rec] = 0;
-          for (int q = 0; q < 3; ++q) { glb(p.shortcut_stats)[3 * rec + q] = 0; glb(p.routing_stats)[3 * rec + q] = 0; }
-          if (p.reuse_stats)
-            for (int q = 0; q < 4; ++q) glb(p.reuse_stats)[4 * rec + q] = 0;
-        }
-      } else {
-        const int end_prev = wave_shr1_int(sk.end, 0);
-        bool ok = !valid || isfinite(sk.objective);
-        if (valid && k > 0) {  // legal_seam, cu:157-161
-          const int jump = sk.start - end_prev;
-          ok = ok && (jump == 0 || jump == 1 || (jump == 2 && sk.skip_ok));
-        }
-        if (__ballot(!ok) == 0) {
-          float total = 0.0f;  // cu:578-584: chunk objectives summed in chunk order
-          for (int i = 0; i < n; ++i) total += readlane_f(sk.objective, i);
-          if (isfinite(total)) {
-            done = 1;
-            const uint64_t shortcut = __ballot(valid && sk.kind == 1);
-            const uint64_t amb = __ballot(valid && sk.kind == 2);
-            const uint64_t dp = __ballot(valid && sk.kind != 1);
-            int frames = valid && sk.kind == 1 ? sk.b - sk.a : 0;
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) frames += __shfl_xor(frames, off, 64);
-            if (k == 0) {
-              glb(p.status)[rec] = 0;
-              glb(p.objective)[rec] = total;
-              glb(p.stitched)[rec] = 1;
-              glb(p.repair_passes)[rec] = 0;
-              glb(p.repaired_frames)[rec] = 0;
-              glb(p.shortcut_stats)[3 * rec + 0] = __popcll(shortcut);
-              glb(p.shortcut_stats)[3 * rec + 1] = frames;
-              glb(p.shortcut_stats)[3 * rec + 2] = __popcll(amb);
-              for (int q = 0; q < 3; ++q) glb(p.routing_stats)[3 * rec + q] = 0;
-              if (p.reuse_stats) {
-                GLB int64_t* u = glb(p.reuse_stats) + 4 * rec;
-                u[0] = 0; u[1] = 0; u[2] = counted ? (int64_t)__popcll(dp) * S : 0; u[3] = 0;
-              }
-            }
-          }
-        }
-      }
-      if (split && done && k == 0) glb(p.tstate)[rec].done = 1;
+      const int done = tail_fast<false>(p, d, rec, glb(p.slots) + d.chunk_offset, n);
+      if (split && done && tid == 0) glb(p.tstate)[rec].done = 1;
       if (tid == 0) h->last = done;
     }
     __syncthreads();
     if (h->last) return;
     __syncthreads();
   }
-  Rec r = make_rec(d, p, L);
-  if (LG) r.st = p.stats + d.frame_offset;
-  if (n <= p.lds_tail_slots) {
-    Slot* ls = reinterpret_cast<Slot*>(lds_raw + ((uintptr_t)L.tslots - (uintptr_t)lds_raw));
-    for (int k = tid; k < n; k += blockDim.x) ls[k] = load_pod(gs + k);
-    __syncthreads();
-    tail_body<K, D, LG>(p, d, rec, r, L, ls, true, p.tail_phase);
-  } else {
-    tail_body<K, D, LG>(p, d, rec, r, L, gs, false, p.tail_phase);
-  }
+  tail_rest<K, D, LG>(p, d, rec, L, p.tail_phase);
 }
 
 // Split tail, after TAIL_PLAN0: one workgroup per (chunk k, record) runs the
@@ -2762,7 +2864,7 @@ enum {
 static_assert(I_WS_TSTATE < 24, "plan->internal holds 24 values");
 
 template <int K, int D, bool LG, class TB>
-int launch_geometry(const ffa::Params& p, const TB& tab, int NT, size_t lds, bool optimized, bool split,
+int launch_geometry(const ffa::Params& p, const TB& tab, int NT, size_t lds, bool optimized, bool split, bool fused,
                     int64_t max_frames, hipStream_t stream) {
   hipEvent_t start = g_profile_start, stop = g_profile_stop;
   g_profile_start = g_profile_stop = nullptr;
@@ -2774,7 +2876,18 @@ int launch_geometry(const ffa::Params& p, const TB& tab, int NT, size_t lds, boo
     hipLaunchKernelGGL((ffa::conventional_kernel<K, D, LG, TB>), dim3(p.count), dim3(NT), lds, stream, p, tab);
   } else {
     const int grid = 8 * ((p.total_slots + 7) / 8);
-    hipLaunchKernelGGL((ffa::chunk_kernel<K, D, LG, TB>), dim3(grid), dim3(std::max(NT, 128)), lds, stream, p, tab);
+    if constexpr (!LG && K <= 16) {
+      if (fused) {  // one launch: the chunk kernel runs each record's tail in its last chunk workgroup
+        hipLaunchKernelGGL((ffa::chunk_kernel<K, D, LG, TB, true>), dim3(grid), dim3(std::max(NT, 128)), lds, stream, p,
+                           tab);
+        if (stop) (void)hipEventRecord(stop, stream);
+        const hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return fail(FFA_E_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
+        return FFA_OK;
+      }
+    }
+    hipLaunchKernelGGL((ffa::chunk_kernel<K, D, LG, TB, false>), dim3(grid), dim3(std::max(NT, 128)), lds, stream, p,
+                       tab);
   }
   if (stop) (void)hipEventRecord(stop, stream);
   if (optimized && split) {  // first-round planning, then one workgroup per first-round interval
@@ -2790,6 +2903,42 @@ int launch_geometry(const ffa::Params& p, const TB& tab, int NT, size_t lds, boo
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(FFA_E_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
   return FFA_OK;
+}
+
+// Arrival counters of the fused tail: FFA_MAX_BATCH ints per (device, stream),
+// zeroed once on the stream when first needed and held until the process
+// ends; every record's last chunk workgroup leaves its counter at zero again.
+// Calls on one stream run in order, so they never use the counters at the same
+// time; calls on different streams have their own. Returns nullptr (the call
+// then takes the two-launch path) while the stream is being captured into a
+// graph and has no counters yet, or when the allocation fails.
+int32_t* arrival_counters(hipStream_t stream) {
+  int device = -1;
+  if (hipGetDevice(&device) != hipSuccess) return nullptr;
+  thread_local int last_device = -1;
+  thread_local hipStream_t last_stream = nullptr;
+  thread_local int32_t* last_counters = nullptr;
+  if (last_counters && device == last_device && stream == last_stream) return last_counters;
+  static std::mutex lock;
+  static std::map<std::pair<int, hipStream_t>, int32_t*> pool;
+  std::lock_guard<std::mutex> guard(lock);
+  auto it = pool.find({device, stream});
+  if (it == pool.end()) {
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone) return nullptr;
+    void* ptr = nullptr;
+    const size_t bytes = sizeof(int32_t) * FFA_MAX_BATCH;
+    if (hipMalloc(&ptr, bytes) != hipSuccess) return nullptr;
+    if (hipMemsetAsync(ptr, 0, bytes, stream) != hipSuccess) {
+      (void)hipFree(ptr);
+      return nullptr;
+    }
+    it = pool.emplace(std::make_pair(device, stream), static_cast<int32_t*>(ptr)).first;
+  }
+  last_device = device;
+  last_stream = stream;
+  last_counters = it->second;
+  return last_counters;
 }
 
 int states_of(const ffa_record& r) { return (int)(2 * r.tokens + 1); }
@@ -3050,9 +3199,13 @@ int ffa_align_describe(const ffa_align_plan* plan, const ffa_record* records, vo
 
 }  // extern "C"
 
-extern "C" int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_options* o, const void* host_table,
-                                const uint8_t* emission_validity, const ffa_align_outputs* out, void* workspace,
-                                hipStream_t stream) {
+namespace {
+
+// ffa_align_launch with the fused tail's arrival counters chosen by the caller
+// (nullptr: chunk and tail kernels as two launches).
+int align_launch(const ffa_align_plan* plan, const ffa_align_options* o, const void* host_table,
+                 const uint8_t* emission_validity, const ffa_align_outputs* out, void* workspace, bool may_fuse,
+                 hipStream_t stream) {
   const int64_t* in = plan->internal;
   const bool optimized = in[I_MODE] != 0;
   if (!host_table || !workspace || !out->labels || !out->scores || !out->status || !out->objective ||
@@ -3103,17 +3256,26 @@ extern "C" int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_opti
   const int64_t max_frames = in[I_MAX_FRAMES];
   const bool split = in[I_SPLIT] != 0;
   p.tstate = split ? reinterpret_cast<ffa::TailState*>(ws + in[I_WS_TSTATE]) : nullptr;
+  // the fused tail: optimized mode with greedy shortcuts, log-probabilities,
+  // no split tail, at most 16 states per thread, and at most four chunks per
+  // CU (larger grids run in several rounds of workgroups, and the hand-off's
+  // wait at each chunk's end would hold back the later rounds: C5's 2,300
+  // chunks measured 1.3% slower fused)
+  const bool fusable = may_fuse && optimized && p.mode == 2 && !p.logits && !split && in[I_K] <= 16 &&
+                       p.total_slots <= 1024;
+  p.arrivals = fusable ? arrival_counters(stream) : nullptr;
+  const bool fused = p.arrivals != nullptr;
   auto run = [&](const auto& tab) -> int {
     using TB = std::decay_t<decltype(tab)>;
     switch (in[I_K]) {
-      case 4: return p.logits ? launch_geometry<4, 8, true, TB>(p, tab, NT, lds, optimized, split, max_frames, stream)
-                              : launch_geometry<4, 8, false, TB>(p, tab, NT, lds, optimized, split, max_frames, stream);
-      case 8: return p.logits ? launch_geometry<8, 6, true, TB>(p, tab, NT, lds, optimized, split, max_frames, stream)
-                              : launch_geometry<8, 6, false, TB>(p, tab, NT, lds, optimized, split, max_frames, stream);
-      case 16: return p.logits ? launch_geometry<16, 4, true, TB>(p, tab, NT, lds, optimized, split, max_frames, stream)
-                               : launch_geometry<16, 4, false, TB>(p, tab, NT, lds, optimized, split, max_frames, stream);
-      case 32: return p.logits ? launch_geometry<32, 1, true, TB>(p, tab, NT, lds, optimized, split, max_frames, stream)
-                               : launch_geometry<32, 1, false, TB>(p, tab, NT, lds, optimized, split, max_frames, stream);
+      case 4: return p.logits ? launch_geometry<4, 8, true, TB>(p, tab, NT, lds, optimized, split, fused, max_frames, stream)
+                              : launch_geometry<4, 8, false, TB>(p, tab, NT, lds, optimized, split, fused, max_frames, stream);
+      case 8: return p.logits ? launch_geometry<8, 6, true, TB>(p, tab, NT, lds, optimized, split, fused, max_frames, stream)
+                              : launch_geometry<8, 6, false, TB>(p, tab, NT, lds, optimized, split, fused, max_frames, stream);
+      case 16: return p.logits ? launch_geometry<16, 4, true, TB>(p, tab, NT, lds, optimized, split, fused, max_frames, stream)
+                               : launch_geometry<16, 4, false, TB>(p, tab, NT, lds, optimized, split, fused, max_frames, stream);
+      case 32: return p.logits ? launch_geometry<32, 1, true, TB>(p, tab, NT, lds, optimized, split, fused, max_frames, stream)
+                               : launch_geometry<32, 1, false, TB>(p, tab, NT, lds, optimized, split, fused, max_frames, stream);
       default: return fail(FFA_E_INVALID, "corrupt plan");
     }
   };
@@ -3128,6 +3290,14 @@ extern "C" int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_opti
   std::memcpy(tab.rec, host_table, plan->table_bytes);
   std::memset(tab.rec + plan->count, 0, sizeof(tab) - plan->table_bytes);
   return run(tab);
+}
+
+}  // namespace
+
+extern "C" int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_options* o, const void* host_table,
+                                const uint8_t* emission_validity, const ffa_align_outputs* out, void* workspace,
+                                hipStream_t stream) {
+  return align_launch(plan, o, host_table, emission_validity, out, workspace, true, stream);
 }
 
 // Allocation-free alignment (ffa_align_launch_noalloc). The descriptor table
@@ -3182,7 +3352,8 @@ extern "C" int ffa_align_launch_noalloc(const ffa_align_plan* plan, const ffa_al
   const int rc = scratch_address(device, &base);
   if (rc != FFA_OK) return rc;
   // nothing in the workspace has to start at zero: every kernel writes what it reads
-  return ffa_align_launch(plan, o, host_table, emission_validity, out, base, stream);
+  // (and the fused tail, whose counters would be a per-stream allocation, is not used)
+  return align_launch(plan, o, host_table, emission_validity, out, base, false, stream);
 }
 
 extern "C" int ffa_token_spans_launch(const ffa_span_record* device_records, int64_t count, const int64_t* labels,

@@ -127,7 +127,13 @@ int ffa_align_describe(const ffa_align_plan* plan, const ffa_record* records,
  * host_table holds the bytes written by ffa_align_describe (see
  * plan->table_uploaded for how long it must live); emission_validity is an
  * optional device bool[B] mask (alignment.cu:946-952); workspace is device
- * memory of plan->workspace_bytes. */
+ * memory of plan->workspace_bytes.
+ * Optimized-mode batches of log-probabilities with at most 1,024 chunks, at
+ * most 4,096 states and no record of 2,048+ frames run as one kernel launch
+ * (the chunk kernel finishes each record itself); for them the library holds
+ * FFA_MAX_BATCH int32 arrival counters (256 KiB) per (device, stream), allocated
+ * and zeroed on the stream's first such call and kept until the process ends.
+ * A stream under graph capture that has none yet takes the two-launch form. */
 int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_options* options,
                      const void* host_table, const uint8_t* emission_validity,
                      const ffa_align_outputs* outputs, void* workspace, hipStream_t stream);
