@@ -2384,7 +2384,8 @@ __device__ __attribute__((always_inline)) void tail_rest(const Params& p, const 
 // was rejected) writes its labels, scores and slot with agent-scope stores
 // and waits for their completion; a chunk that ran a DP wrote backpointers,
 // frontiers and its path with ordinary stores and releases them at agent
-// scope (an L2 write-back, which only the rarer DP chunks pay). Then one
+// scope (thread 0's release-ordered count: one L2 write-back, which only the
+// rarer DP chunks pay). Every wave first waits for its own stores. Then one
 // arrival on the record's counter; the last one zeroes it for the next call.
 // The tail's fast path reads the slots with agent-scope loads; the full tail
 // first acquires at agent scope.
@@ -2552,9 +2553,8 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p, TB
     Header* h = L.h;
     const int chunks = (int)(1 + (d.frames - 1) / p.H);
     if (tid == 0) store_pod_agent(glb(p.slots) + slot_index, out);
-    if (ran_dp) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    else wait_stores();
-    __syncthreads();
+    wait_stores();  // every wave's stores are complete (in this XCD's L2, or written through) ...
+    __syncthreads();  // ... before thread 0 counts; for a DP chunk its count is a release (one L2 write-back)
     if (tid == 0) {
       const int old = ran_dp ? __hip_atomic_fetch_add(p.arrivals + rec, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT)
                              : __hip_atomic_fetch_add(p.arrivals + rec, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
