@@ -2328,9 +2328,10 @@ __device__ __attribute__((always_inline)) int tail_fast(const Params& p, const R
         const uint64_t shortcut = __ballot(valid && sk.kind == 1);
         const uint64_t amb = __ballot(valid && sk.kind == 2);
         const uint64_t dp = __ballot(valid && sk.kind != 1);
-        int frames = valid && sk.kind == 1 ? sk.b - sk.a : 0;
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) frames += __shfl_xor(frames, off, 64);
+        // shortcut frames: H per shortcut chunk, the last chunk's own length for it
+        const uint64_t last_bit = 1ull << (n - 1);
+        const int64_t frames = (int64_t)p.H * __popcll(shortcut & ~last_bit) +
+                               ((shortcut & last_bit) ? (int64_t)d.frames - (int64_t)(n - 1) * p.H : 0);
         if (k == 0) {
           glb(p.status)[rec] = 0;
           glb(p.objective)[rec] = total;
@@ -3201,10 +3202,11 @@ int ffa_align_describe(const ffa_align_plan* plan, const ffa_record* records, vo
 
 namespace {
 
-// ffa_align_launch with the fused tail's arrival counters chosen by the caller
-// (nullptr: chunk and tail kernels as two launches).
+// ffa_align_launch with the fused tail's arrival counters chosen by the caller:
+// `counters` (FFA_MAX_BATCH zeroed ints) or, when it is null, the stream's own
+// (arrival_counters).
 int align_launch(const ffa_align_plan* plan, const ffa_align_options* o, const void* host_table,
-                 const uint8_t* emission_validity, const ffa_align_outputs* out, void* workspace, bool may_fuse,
+                 const uint8_t* emission_validity, const ffa_align_outputs* out, void* workspace, int32_t* counters,
                  hipStream_t stream) {
   const int64_t* in = plan->internal;
   const bool optimized = in[I_MODE] != 0;
@@ -3261,9 +3263,8 @@ int align_launch(const ffa_align_plan* plan, const ffa_align_options* o, const v
   // CU (larger grids run in several rounds of workgroups, and the hand-off's
   // wait at each chunk's end would hold back the later rounds: C5's 2,300
   // chunks measured 1.3% slower fused)
-  const bool fusable = may_fuse && optimized && p.mode == 2 && !p.logits && !split && in[I_K] <= 16 &&
-                       p.total_slots <= 1024;
-  p.arrivals = fusable ? arrival_counters(stream) : nullptr;
+  const bool fusable = optimized && p.mode == 2 && !p.logits && !split && in[I_K] <= 16 && p.total_slots <= 1024;
+  p.arrivals = !fusable ? nullptr : counters ? counters : arrival_counters(stream);
   const bool fused = p.arrivals != nullptr;
   auto run = [&](const auto& tab) -> int {
     using TB = std::decay_t<decltype(tab)>;
@@ -3297,7 +3298,7 @@ int align_launch(const ffa_align_plan* plan, const ffa_align_options* o, const v
 extern "C" int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_options* o, const void* host_table,
                                 const uint8_t* emission_validity, const ffa_align_outputs* out, void* workspace,
                                 hipStream_t stream) {
-  return align_launch(plan, o, host_table, emission_validity, out, workspace, true, stream);
+  return align_launch(plan, o, host_table, emission_validity, out, workspace, nullptr, stream);
 }
 
 // Allocation-free alignment (ffa_align_launch_noalloc). The descriptor table
@@ -3306,25 +3307,35 @@ extern "C" int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_opti
 // device memory: the host only ever uses the per-device address that
 // hipGetSymbolAddress returns for it.
 static __device__ __align__(256) unsigned char scratch[FFA_NOALLOC_MAX_BYTES];
+// The fused tail's arrival counters of that entry, one per record: zero when
+// the library is loaded, and every call leaves them at zero again.
+static __device__ __align__(256) int32_t arrival_scratch[FFA_MAX_BATCH];
 
 namespace {
 
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_lock;
 void* g_scratch_ptr[kMaxDevices] = {};
+void* g_arrival_ptr[kMaxDevices] = {};
 
-// The device address of `scratch` on the current device `device`, looked up
-// once per device (with that device current) and kept.
-int scratch_address(int device, unsigned char** out) {
+// The device addresses of `scratch` and `arrival_scratch` on the current
+// device `device`, looked up once per device (with that device current) and kept.
+int scratch_address(int device, unsigned char** out, int32_t** arrivals) {
   std::lock_guard<std::mutex> lock(g_scratch_lock);
   if (!g_scratch_ptr[device]) {
     void* ptr = nullptr;
-    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (err != hipSuccess || !ptr)
       return fail(FFA_E_HIP, std::string("scratch address lookup failed: ") + hipGetErrorString(err));
+    void* counters = nullptr;
+    err = hipGetSymbolAddress(&counters, HIP_SYMBOL(arrival_scratch));
+    if (err != hipSuccess || !counters)
+      return fail(FFA_E_HIP, std::string("scratch address lookup failed: ") + hipGetErrorString(err));
+    g_arrival_ptr[device] = counters;
     g_scratch_ptr[device] = ptr;
   }
   *out = static_cast<unsigned char*>(g_scratch_ptr[device]);
+  *arrivals = static_cast<int32_t*>(g_arrival_ptr[device]);
   return FFA_OK;
 }
 
@@ -3349,11 +3360,12 @@ extern "C" int ffa_align_launch_noalloc(const ffa_align_plan* plan, const ffa_al
     if (stream_device != device) return fail(FFA_E_INVALID, "the stream belongs to another device than the current one");
   }
   unsigned char* base = nullptr;
-  const int rc = scratch_address(device, &base);
+  int32_t* arrivals = nullptr;
+  const int rc = scratch_address(device, &base, &arrivals);
   if (rc != FFA_OK) return rc;
-  // nothing in the workspace has to start at zero: every kernel writes what it reads
-  // (and the fused tail, whose counters would be a per-stream allocation, is not used)
-  return align_launch(plan, o, host_table, emission_validity, out, base, false, stream);
+  // nothing in the workspace has to start at zero: every kernel writes what it
+  // reads; the fused tail's counters start at zero and every call leaves them so
+  return align_launch(plan, o, host_table, emission_validity, out, base, arrivals, stream);
 }
 
 extern "C" int ffa_token_spans_launch(const ffa_span_record* device_records, int64_t count, const int64_t* labels,

@@ -151,7 +151,10 @@ int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_options* option
  * 9,000 tokens need 580 MiB and must use ffa_align_launch).
  * Every call on a GPU shares that GPU's array: calls enqueued on one stream
  * are ordered, but calls that overlap on one GPU (several streams or threads)
- * race and corrupt each other's results. */
+ * race and corrupt each other's results. Batches that ffa_align_launch runs
+ * as one launch run so here too, with their arrival counters in a second
+ * device array of FFA_MAX_BATCH int32 per GPU (zero when the library loads,
+ * left at zero by every call). */
 #define FFA_NOALLOC_MAX_BYTES (32u << 20)
 int ffa_align_launch_noalloc(const ffa_align_plan* plan, const ffa_align_options* options, const void* host_table,
                              const uint8_t* emission_validity, const ffa_align_outputs* outputs,

@@ -1,7 +1,10 @@
 """The allocation-free entry point (ffa_align_launch_noalloc): its outputs
-equal ffa_align_launch's bit for bit, on two calls in a row whose second batch
-is smaller (the shared device array keeps the first call's contents), and a
-batch beyond its fixed scratch is refused."""
+equal ffa_align_launch's bit for bit, on calls in a row whose later batches
+are smaller (the shared device array keeps the first call's contents): a
+1,024-record batch (chunk and tail kernels), then two batches that run as one
+launch with the fused tail, whose arrival counters live in a second fixed
+array (12 C2 records, then C1, whose records are repaired); and a batch beyond
+its fixed scratch is refused."""
 from __future__ import annotations
 
 import ctypes
@@ -71,7 +74,8 @@ def test_noalloc_matches_launch_on_two_calls(optimized):
     lib = capi.load()
     big = _device(workloads.make("c5"))        # 1,024 records: ~11 MiB of scratch
     small = _device(workloads.c2(batch=12))    # then a smaller batch over the stale contents
-    for name, (es, ys) in (("c5", big), ("c2x12", small)):
+    tiny = _device(workloads.c1())             # fused tail with repairs, counters left by the last call
+    for name, (es, ys) in (("c5", big), ("c2x12", small), ("c1", tiny)):
         print(f"noalloc {name} optimized={optimized}", flush=True)
         want = _run(lib, es, ys, optimized, noalloc=False)
         got = _run(lib, es, ys, optimized, noalloc=True)
