@@ -1951,10 +1951,7 @@ __device__ inline int xcd_slot(int bid, int total) {
   return (bid % 8) * per + bid / 8;
 }
 
-// Optimized mode, one workgroup per record, after the chunk kernel: repair
-// rounds, seam validation, full-DP fallback, final path and every per-record
-// output (plan_repairs cu:164-228, repair DP cu:727-760, validate_seams
-// cu:562-592, fallback_recurrence cu:552-559, finish cu:642-667).
+// A chunk slot, from LDS or from global memory (the tail's two slot arrays).
 __device__ inline Slot load_slot(const Slot* x) { return *x; }
 __device__ inline Slot load_slot(const GLB Slot* x) { return load_pod(x); }
 
