@@ -141,6 +141,11 @@ struct Params {
   struct TailState* tstate;  // split tail: per-record state between its phases
   int32_t* arrivals;         // fused tail: per-record count of finished chunks, zero between calls
 };
+// Fused tail: at most this many chunks (so records) per batch, and one arrival
+// counter per 128-byte line (the records' counters are hit by every chunk
+// workgroup at nearly the same time; on shared lines the atomics queue).
+constexpr int FUSED_MAX_CHUNKS = 1024;
+constexpr int ARRIVAL_STRIDE = 32;
 
 // ---------------------------------------------------------------------------
 // Shared-memory layout. A fixed header followed by dynamic regions whose sizes
@@ -2554,10 +2559,11 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) chunk_kernel(Params p, TB
     wait_stores();  // every wave's stores are complete (in this XCD's L2, or written through) ...
     __syncthreads();  // ... before thread 0 counts; for a DP chunk its count is a release (one L2 write-back)
     if (tid == 0) {
-      const int old = ran_dp ? __hip_atomic_fetch_add(p.arrivals + rec, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT)
-                             : __hip_atomic_fetch_add(p.arrivals + rec, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      int32_t* counter = p.arrivals + rec * ARRIVAL_STRIDE;
+      const int old = ran_dp ? __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT)
+                             : __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       const int last = old == chunks - 1;
-      if (last) __hip_atomic_store(p.arrivals + rec, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       h->arrived = last;
     }
     __syncthreads();
@@ -2903,7 +2909,8 @@ int launch_geometry(const ffa::Params& p, const TB& tab, int NT, size_t lds, boo
   return FFA_OK;
 }
 
-// Arrival counters of the fused tail: FFA_MAX_BATCH ints per (device, stream),
+// Arrival counters of the fused tail: 128 KiB per (device, stream) (one counter
+// per 128-byte line for each of up to FUSED_MAX_CHUNKS records),
 // zeroed once on the stream when first needed and held until the process
 // ends; every record's last chunk workgroup leaves its counter at zero again.
 // Calls on one stream run in order, so they never use the counters at the same
@@ -2925,7 +2932,7 @@ int32_t* arrival_counters(hipStream_t stream) {
     hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(stream, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone) return nullptr;
     void* ptr = nullptr;
-    const size_t bytes = sizeof(int32_t) * FFA_MAX_BATCH;
+    const size_t bytes = sizeof(int32_t) * ffa::FUSED_MAX_CHUNKS * ffa::ARRIVAL_STRIDE;
     if (hipMalloc(&ptr, bytes) != hipSuccess) return nullptr;
     if (hipMemsetAsync(ptr, 0, bytes, stream) != hipSuccess) {
       (void)hipFree(ptr);
@@ -3260,7 +3267,8 @@ int align_launch(const ffa_align_plan* plan, const ffa_align_options* o, const v
   // CU (larger grids run in several rounds of workgroups, and the hand-off's
   // wait at each chunk's end would hold back the later rounds: C5's 2,300
   // chunks measured 1.3% slower fused)
-  const bool fusable = optimized && p.mode == 2 && !p.logits && !split && in[I_K] <= 16 && p.total_slots <= 1024;
+  const bool fusable = optimized && p.mode == 2 && !p.logits && !split && in[I_K] <= 16 &&
+                       p.total_slots <= ffa::FUSED_MAX_CHUNKS;
   p.arrivals = !fusable ? nullptr : counters ? counters : arrival_counters(stream);
   const bool fused = p.arrivals != nullptr;
   auto run = [&](const auto& tab) -> int {
@@ -3304,9 +3312,10 @@ extern "C" int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_opti
 // device memory: the host only ever uses the per-device address that
 // hipGetSymbolAddress returns for it.
 static __device__ __align__(256) unsigned char scratch[FFA_NOALLOC_MAX_BYTES];
-// The fused tail's arrival counters of that entry, one per record: zero when
+// The fused tail's arrival counters of that entry (one per record, each on its
+// own 128-byte line): zero when
 // the library is loaded, and every call leaves them at zero again.
-static __device__ __align__(256) int32_t arrival_scratch[FFA_MAX_BATCH];
+static __device__ __align__(256) int32_t arrival_scratch[ffa::FUSED_MAX_CHUNKS * ffa::ARRIVAL_STRIDE];
 
 namespace {
 

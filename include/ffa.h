@@ -131,8 +131,9 @@ int ffa_align_describe(const ffa_align_plan* plan, const ffa_record* records,
  * Optimized-mode batches of log-probabilities with at most 1,024 chunks, at
  * most 4,096 states and no record of 2,048+ frames run as one kernel launch
  * (the chunk kernel finishes each record itself); for them the library holds
- * FFA_MAX_BATCH int32 arrival counters (256 KiB) per (device, stream), allocated
- * and zeroed on the stream's first such call and kept until the process ends.
+ * 128 KiB of arrival counters per (device, stream) (one per 128-byte line for
+ * up to 1,024 records), allocated and zeroed on the stream's first such call
+ * and kept until the process ends.
  * A stream under graph capture that has none yet takes the two-launch form. */
 int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_options* options,
                      const void* host_table, const uint8_t* emission_validity,
@@ -153,8 +154,8 @@ int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_options* option
  * are ordered, but calls that overlap on one GPU (several streams or threads)
  * race and corrupt each other's results. Batches that ffa_align_launch runs
  * as one launch run so here too, with their arrival counters in a second
- * device array of FFA_MAX_BATCH int32 per GPU (zero when the library loads,
- * left at zero by every call). */
+ * device array of 128 KiB per GPU (zero when the library loads, left at zero
+ * by every call). */
 #define FFA_NOALLOC_MAX_BYTES (32u << 20)
 int ffa_align_launch_noalloc(const ffa_align_plan* plan, const ffa_align_options* options, const void* host_table,
                              const uint8_t* emission_validity, const ffa_align_outputs* outputs,
