@@ -45,6 +45,33 @@ void check_ffa(int rc) {
 
 int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
+// The workspace of a call on `stream`: kept per thread and stream between calls
+// up to 64 MiB (the kernels of calls on one stream run in order, so the next
+// call may reuse it; workspaces past the cap, and calls under graph capture,
+// allocate per call). The cache is never destroyed: tensors must not be freed
+// after the allocator at exit.
+at::Tensor workspace_for(const at::TensorOptions& options, int64_t bytes, hipStream_t stream) {
+  constexpr int64_t kCap = int64_t(64) << 20;
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  // under graph capture the workspace comes from the graph's own pool, as before
+  if (bytes > kCap || hipStreamIsCapturing(stream, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone)
+    return at::empty({bytes}, options.dtype(at::kByte));
+  struct Entry {
+    c10::DeviceIndex device;
+    hipStream_t stream;
+    at::Tensor buffer;
+  };
+  static thread_local auto* cache = new std::vector<Entry>();
+  const c10::DeviceIndex device = options.device().index();
+  for (Entry& e : *cache)
+    if (e.device == device && e.stream == stream) {
+      if (e.buffer.numel() < bytes) e.buffer = at::empty({bytes}, options.dtype(at::kByte));
+      return e.buffer;
+    }
+  cache->push_back({device, stream, at::empty({bytes}, options.dtype(at::kByte))});
+  return cache->back().buffer;
+}
+
 // A tensor over bytes [offset, offset + numel*itemsize) of `block`: shares the
 // block's storage (one allocation serves every output of a call).
 at::Tensor view_of(const at::Tensor& block, int64_t offset, at::ScalarType type, c10::IntArrayRef sizes) {
@@ -132,7 +159,7 @@ std::tuple<std::vector<at::Tensor>, std::vector<int64_t>> run_align(int64_t coun
   }
   check_ffa(ffa_align_describe(&plan, records.data(), table, plan.table_bytes));
   const auto options = e0.options();
-  auto scratch = at::empty({plan.workspace_bytes}, options.dtype(at::kByte));
+  auto scratch = workspace_for(options, plan.workspace_bytes, stream.stream());
   // outputs: one allocation, ten views (alignment.cu:1059 order)
   const int64_t N = plan.total_frames, B = count, R = plan.reuse_rows;
   int64_t off = 0;
