@@ -449,7 +449,11 @@ def main() -> int:
         achieved = min_bytes / (kernel_ms * 1e-3) / 1e9
         return step_s, kernel_ms, achieved, result
 
-    kernel_name = "chunk_kernel" if args.mode == "optimized" else "conventional_kernel"
+    # conventional mode cuts transcripts of more than 4,096 states into bands of
+    # 256 states, one single-wave workgroup each (band_kernel, ffa_kernels.hip)
+    states = [2 * len(y) + 1 for y in batch.targets]
+    banded = args.mode == "conventional" and max(states) > 4096
+    kernel_name = "chunk_kernel" if args.mode == "optimized" else "band_kernel" if banded else "conventional_kernel"
     # optimized mode runs each record's tail inside the chunk kernel (one launch
     # per call) for batches of log-probabilities with at most 1,024 chunks, at
     # most 4,096 states and no record of 2,048+ frames (the split tail's
@@ -492,7 +496,7 @@ def main() -> int:
     # the same timing of an empty kernel with the dominant kernel's workgroup
     # count, and the fraction a kernel of exactly that duration would reach
     groups = 8 * ((sum((e.shape[0] + 127) // 128 for e in batch.emissions) + 7) // 8) \
-        if args.mode == "optimized" else len(es)
+        if args.mode == "optimized" else sum((s + 255) // 256 for s in states) if banded else len(es)
     floor_us = launch_floor(capi_lib, hip, groups, args.steps)
     line["roofline"]["launch_floor_us"] = floor_us
     line["roofline"]["frac_ceiling"] = min_bytes / (floor_us * 1e-6) / 1e9 / HBM_PEAK_GBS

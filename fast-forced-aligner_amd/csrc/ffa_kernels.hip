@@ -140,6 +140,9 @@ struct Params {
   float2* stats;        // logits: per frame {row max, log of the row's exp-sum}, indexed like labels
   struct TailState* tstate;  // split tail: per-record state between its phases
   int32_t* arrivals;         // fused tail: per-record count of finished chunks, zero between calls
+  int32_t* band_ctl;         // banded DP: ticket, late flag, per-record arrivals, terminal values (zeroed per call)
+  uint64_t* edges;           // banded DP: per record and band boundary, one tagged value per frame
+  int32_t band_stride;       // banded DP: edge arrays per frame of the batch (bands of the widest record - 1)
 };
 // Fused tail: at most this many chunks (so records) per batch, and one arrival
 // counter per 128-byte line (the records' counters are hit by every chunk
@@ -1949,6 +1952,239 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) conventional_kernel(Param
   if (!ok) write_failed(r, 0, r.T);
 }
 
+// ---------------------------------------------------------------------------
+// Banded DP: conventional mode for batches with transcripts of more than 4,096
+// states. A record's states are cut into bands of BAND_STATES, one wave each
+// (BAND_K contiguous states per lane), and every band is a workgroup of its
+// own, so a record of 18,001 states runs on 71 CUs instead of one. State s at
+// frame t reads states s, s-1 and s-2 at frame t-1 (cu:438-444); a band's first
+// state is even (a blank state, which no skip enters, cu:407), so all a band
+// needs from outside is the previous band's last state at frame t-1. Band j
+// publishes that value for every frame as one 8-byte entry of its edge array
+// (the float and a valid tag, an agent-scope store written through to
+// memory); band j+1 loads the entry BAND_D frames ahead with an agent-scope
+// load and checks the tag at use, so it runs a few frames behind band j. The
+// edge arrays and control words are zeroed before each call (zero_kernel).
+// Workgroups take their band from a ticket counter in the order they start,
+// so band j-1 is running whenever band j waits for it and every wait ends;
+// a wait is bounded all the same (BAND_SPIN_LIMIT polls of one entry, then
+// the band waits no more, uses NaN and flags the call in control word 1).
+// Each band writes its lanes' part of every backpointer row (the layout of
+// the one-workgroup DP: thread index band*64+lane with BAND_K states), then
+// counts itself on the record's arrival counter with a release; the last band
+// to arrive acquires, selects the terminal state (cu:497-500), walks the path
+// (finish, cu:642-667) and writes the record's outputs.
+constexpr int BAND_K = 4;  // a one-wave frame of K = 4 measured 317 ns, of K = 8 362 ns
+constexpr int BAND_STATES = 64 * BAND_K;
+constexpr int BAND_D = 16;                // frames of gathers and edge loads in flight
+constexpr int BAND_SPIN_LIMIT = 1 << 21;  // polls of one entry (about a second) before a band stops waiting
+constexpr int BAND_CTL_HEAD = 64;         // control words: [0] ticket, [1] a wait ran out, then an arrival count per record
+
+__device__ inline uint64_t edge_load(const GLB uint64_t* at) {
+  return __hip_atomic_load((const uint64_t*)at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The previous band's value in entry `ent` (loaded ahead from `at`), polling
+// the entry while its tag is unset. `late`: a wait of this band ran out.
+__device__ inline float edge_value(uint64_t ent, const GLB uint64_t* at, int& late, int32_t* ctl) {
+  uint32_t tag = __builtin_amdgcn_readfirstlane((uint32_t)(ent >> 32));
+  uint32_t val = __builtin_amdgcn_readfirstlane((uint32_t)ent);
+  if (tag != 1u) {
+    if (!late) {
+      for (int spins = 0; spins < BAND_SPIN_LIMIT; ++spins) {
+        __builtin_amdgcn_s_sleep(8);
+        const uint64_t again = edge_load(at);
+        tag = __builtin_amdgcn_readfirstlane((uint32_t)(again >> 32));
+        val = __builtin_amdgcn_readfirstlane((uint32_t)again);
+        if (tag == 1u) break;
+      }
+    }
+    if (tag != 1u) {
+      if (!late && threadIdx.x == 0) __hip_atomic_store(ctl + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      late = 1;
+      return __builtin_nanf("");
+    }
+  }
+  return __uint_as_float(val);
+}
+
+// The per-record outputs of conventional mode besides the path.
+__device__ inline void conventional_outputs(const Params& p, int rec, int status, float objective) {
+  glb(p.status)[rec] = status;
+  glb(p.objective)[rec] = objective;
+  glb(p.stitched)[rec] = 0;
+  glb(p.repair_passes)[rec] = 0;
+  glb(p.repaired_frames)[rec] = 0;
+  for (int q = 0; q < 3; ++q) { glb(p.shortcut_stats)[3 * rec + q] = 0; glb(p.routing_stats)[3 * rec + q] = 0; }
+}
+
+template <class TB>
+__global__ void __launch_bounds__(64) band_kernel(Params p, TB tab) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  const Lds L = carve(lds_raw, p);
+  const int lane = threadIdx.x;
+  int ticket = 0;
+  if (lane == 0) ticket = __hip_atomic_fetch_add(p.band_ctl, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  ticket = __builtin_amdgcn_readlane(ticket, 0);
+  // ticket -> (record, band): bands are numbered record by record
+  int rec = -1, band = 0, bands = 1;
+  for (int g = 0, base = 0; g < p.count; g += 64) {
+    const int i = g + lane;
+    int nb = 0;
+    if (i < p.count) {
+      int U;
+      if constexpr (kArgs<TB>) U = tab.rec[i].tokens;
+      else U = glb(p.desc)[i].tokens;
+      nb = (2 * U + 1 + BAND_STATES - 1) / BAND_STATES;
+    }
+    const int incl = wave_incl_scan(nb);
+    const uint64_t hit = __ballot(i < p.count && ticket < base + incl);
+    if (hit) {
+      const int l = (int)__builtin_ctzll(hit);
+      rec = g + l;
+      bands = __builtin_amdgcn_readlane(nb, l);
+      band = ticket - (base + __builtin_amdgcn_readlane(incl, l) - bands);
+      break;
+    }
+    base += __builtin_amdgcn_readlane(incl, 63);
+  }
+  if (rec < 0) return;  // (the grid has one workgroup per band)
+  RecordDesc d;
+  if constexpr (kArgs<TB>) d = tab.rec[rec];
+  else d = load_pod(glb(p.desc) + rec);
+  Rec r = make_rec(d, p, L);
+  const Staged st = stage_tokens<ALPHABET_NONE>(d, p, rec, L);
+  const int S = r.S;
+  const int64_t T = r.T;
+  if (st.status >= 2) {  // every band sees the same status; the first writes the outputs (cu:642-652)
+    if (band == 0) {
+      if (lane == 0) conventional_outputs(p, rec, st.status, NEG_INF);
+      write_failed(r, 0, T);
+    }
+    return;
+  }
+  constexpr int K = BAND_K;
+  const int s0 = band * BAND_STATES + lane * K;
+  const int gtid = band * 64 + lane;
+  const bool active = s0 < S;
+  uint32_t lab[K];
+  float skb[K];  // 0 where the skip transition is legal, -inf elsewhere (cu:407)
+  float al[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int s = s0 + k;
+    const int ls = s < S ? label_of(r, s) : r.blank;
+    lab[k] = 4u * (uint32_t)ls;
+    const bool ok = s >= 2 && s < S && ls != r.blank && ls != label_of(r, s - 2);
+    skb[k] = ok ? 0.0f : NEG_INF;
+  }
+  const GLB float* e = r.e;
+  const int64_t V = r.V;
+  GLB uint32_t* bp = r.bp;
+  const int64_t stride = r.stride;
+  const bool has_next = band + 1 < bands;
+  GLB uint64_t* edges = glb(p.edges) + d.frame_offset * (int64_t)p.band_stride;
+  const GLB uint64_t* ein = band > 0 ? edges + (int64_t)(band - 1) * T : nullptr;
+  GLB uint64_t* eout = edges + (int64_t)band * T;  // written only when has_next
+  int32_t* ctl = p.band_ctl;
+  // frame 0 (cu:409-410)
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const float v = ldg_at(e, lab[k]);
+    al[k] = (s0 + k < S && s0 + k < 2) ? v : NEG_INF;
+  }
+  if (active) store_row<K>(bp, gtid, 0u);
+  if (has_next && lane == 63)
+    __hip_atomic_store((uint64_t*)eout, (uint64_t)__float_as_uint(al[K - 1]) | (1ull << 32), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  int late = 0;
+  // one frame of the recurrence (cu:438-444); strict '>' keeps stay > advance > skip on ties
+  auto frame = [&](int64_t t, const float (&evk)[K], float fill) {
+    const float up1 = wave_shr1(al[K - 1], fill);
+    uint32_t bits = 0;
+#pragma unroll
+    for (int k = K - 1; k >= 0; --k) {
+      const float stay = al[k];
+      const float adv = k >= 1 ? al[k - 1] : up1;
+      const float skp = k >= 2 ? al[k - 2] : up1;
+      float best = stay;
+      uint32_t j = 0;
+      if (adv > best) { best = adv; j = 1; }
+      bool take = false;
+      if ((k & 1) != 0) take = skp + skb[k] > best;  // even states are blank states: no skip into them
+      if (take) { best = skp; j = 2; }
+      al[k] = best + evk[k];
+      bits |= j << (2 * k);
+    }
+    if (active) store_row<K>(bp + t * stride, gtid, bits);
+    if (has_next && lane == 63)
+      __hip_atomic_store((uint64_t*)(eout + t), (uint64_t)__float_as_uint(al[K - 1]) | (1ull << 32),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  if (T > 1) {
+    const int64_t last = T - 1;
+    float ev[BAND_D][K];
+    uint64_t eg[BAND_D];
+#pragma unroll
+    for (int dd = 0; dd < BAND_D; ++dd) {
+      const int64_t t = min((int64_t)1 + dd, last);
+      const GLB float* row = e + t * V;
+#pragma unroll
+      for (int k = 0; k < K; ++k) ev[dd][k] = ldg_at(row, lab[k]);
+      eg[dd] = ein ? edge_load(ein + t - 1) : 0ull;
+    }
+    auto fill_of = [&](int dd, int64_t t) -> float {
+      return ein ? edge_value(eg[dd], ein + t - 1, late, ctl) : NEG_INF;
+    };
+    int64_t t0 = 1;
+    for (; t0 + BAND_D <= T; t0 += BAND_D) {
+#pragma unroll
+      for (int dd = 0; dd < BAND_D; ++dd) {
+        const int64_t t = t0 + dd;
+        frame(t, ev[dd], fill_of(dd, t));
+        const int64_t tn = min(t + BAND_D, last);
+        const GLB float* row = e + tn * V;
+#pragma unroll
+        for (int k = 0; k < K; ++k) ev[dd][k] = ldg_at(row, lab[k]);
+        if (ein) eg[dd] = edge_load(ein + tn - 1);
+      }
+    }
+#pragma unroll
+    for (int dd = 0; dd < BAND_D; ++dd)
+      if (t0 + dd < T) frame(t0 + dd, ev[dd], fill_of(dd, t0 + dd));
+  }
+  // the terminal candidates S-1 and S-2 (cu:497-500), from whichever band holds them
+  GLB float* term = reinterpret_cast<GLB float*>(glb(ctl) + BAND_CTL_HEAD + p.count) + 2 * (int64_t)rec;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int s = s0 + k;
+    if (s == S - 1) __hip_atomic_store((float*)term + 1, al[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (S > 1 && s == S - 2) __hip_atomic_store((float*)term, al[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  wait_stores();  // this band's rows and values are complete before its release
+  int last_band = 0;
+  if (lane == 0)
+    last_band = __hip_atomic_fetch_add(ctl + BAND_CTL_HEAD + rec, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT) ==
+                bands - 1;
+  if (!__builtin_amdgcn_readlane(last_band, 0)) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  const float v1 = __hip_atomic_load((float*)term + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const float v0 = S > 1 ? __hip_atomic_load((float*)term, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : NEG_INF;
+  int terminal = S - 1;
+  float score = v1;
+  if (S > 1 && v0 >= v1) { terminal = S - 2; score = v0; }
+  const bool ok = isfinite(score);
+  if (ok) (void)trace_path(r, 0, T, terminal);
+  if (lane == 0) conventional_outputs(p, rec, ok ? 0 : 1, score);  // cu:507-510
+  if (!ok) write_failed(r, 0, T);
+}
+
+// Zeroes n 16-byte words (the banded DP's control words and edge arrays).
+__global__ void __launch_bounds__(256) zero_kernel(v4i_t* dst, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    glb(dst)[i] = v4i_t{0, 0, 0, 0};
+}
+
 // XCD-aware placement: workgroup i runs on XCD i % 8, so consecutive slots of
 // one record (which share its targets) are mapped to the same XCD's L2.
 __device__ inline int xcd_slot(int bid, int total) {
@@ -2863,20 +3099,35 @@ inline int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 enum {
   I_K, I_NT, I_SLOTS, I_LDS, I_UCAP, I_DCAP, I_VWORDS, I_TAILSLOTS, I_FRONTIER, I_BUDGET,
   I_OVERLAP, I_WS_SLOTS, I_WS_FRONTIER, I_MODE, I_H, I_FMIN, I_REPAIR_MIN, I_EBLK, I_LOGITS, I_WS_STATS,
-  I_MAX_FRAMES, I_WS_BP, I_SPLIT, I_WS_TSTATE
+  I_MAX_FRAMES, I_WS_BP, I_SPLIT, I_WS_TSTATE, I_BANDS, I_BAND_STRIDE, I_WS_BAND, I_BAND_BYTES, I_BAND_LDS
 };
-static_assert(I_WS_TSTATE < 24, "plan->internal holds 24 values");
+static_assert(I_BAND_LDS < 32, "plan->internal holds 32 values");
+
+// Banded DP launch (conventional mode, transcripts of more than 4,096 states):
+// workgroups (one per band), LDS bytes, and the 16-byte words zeroed first.
+struct BandLaunch {
+  int64_t bands;
+  size_t lds;
+  int64_t zero_words;
+};
 
 template <int K, int D, bool LG, class TB>
 int launch_geometry(const ffa::Params& p, const TB& tab, int NT, size_t lds, bool optimized, bool split, bool fused,
-                    int64_t max_frames, hipStream_t stream) {
+                    int64_t max_frames, const BandLaunch& band, hipStream_t stream) {
   hipEvent_t start = g_profile_start, stop = g_profile_stop;
   g_profile_start = g_profile_stop = nullptr;
   if (p.logits && !optimized)
     hipLaunchKernelGGL(ffa::stats_kernel<TB>, dim3((unsigned)((max_frames + 127) / 128), (unsigned)p.count), dim3(256),
                        0, stream, p, tab);
+  if (!optimized && band.bands > 0) {  // zeroed control words and edge arrays, then one workgroup per band
+    const int64_t blocks = std::min<int64_t>(2048, (band.zero_words + 255) / 256);
+    hipLaunchKernelGGL(ffa::zero_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       reinterpret_cast<ffa::v4i_t*>(p.band_ctl), band.zero_words);
+  }
   if (start) (void)hipEventRecord(start, stream);
-  if (!optimized) {
+  if (!optimized && band.bands > 0) {
+    hipLaunchKernelGGL(ffa::band_kernel<TB>, dim3((unsigned)band.bands), dim3(64), band.lds, stream, p, tab);
+  } else if (!optimized) {
     hipLaunchKernelGGL((ffa::conventional_kernel<K, D, LG, TB>), dim3(p.count), dim3(NT), lds, stream, p, tab);
   } else {
     const int grid = 8 * ((p.total_slots + 7) / 8);
@@ -3111,6 +3362,24 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
   if (split) ws += align_up((int64_t)sizeof(ffa::TailState) * count, 256);
   const int64_t ws_stats = ws;
   if (logits) ws += align_up(8 * total_frames, 256);
+  // banded DP (conventional mode, log-probabilities, more than 4,096 states):
+  // control words (ticket, late flag, arrival counts, terminal values) and
+  // the edge arrays (8 bytes per frame and band boundary of the widest record)
+  int64_t bands = 0, band_stride = 0, band_bytes = 0, band_lds = 0;
+  const int64_t ws_band = ws;
+  if (!optimized && !logits && K == 32) {
+    int64_t nb_max = 1;
+    for (int64_t i = 0; i < count; ++i) {
+      const int64_t nb = (states_of(records[i]) + ffa::BAND_STATES - 1) / ffa::BAND_STATES;
+      bands += nb;
+      nb_max = std::max(nb_max, nb);
+    }
+    band_stride = nb_max - 1;
+    band_bytes = align_up(4 * (ffa::BAND_CTL_HEAD + count) + 8 * count, 256) + 8 * total_frames * band_stride;
+    band_bytes = align_up(band_bytes, 256);
+    ws += band_bytes;
+    band_lds = align_up((int64_t)sizeof(ffa::Header), 16) + targets;
+  }
   std::memset(plan, 0, sizeof(*plan));
   plan->count = count;
   plan->total_frames = total_frames;
@@ -3143,6 +3412,11 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
   in[I_WS_BP] = ws_bp;
   in[I_SPLIT] = split ? 1 : 0;
   in[I_WS_TSTATE] = ws_tstate;
+  in[I_BANDS] = bands;
+  in[I_BAND_STRIDE] = band_stride;
+  in[I_WS_BAND] = ws_band;
+  in[I_BAND_BYTES] = band_bytes;
+  in[I_BAND_LDS] = band_lds;
   return FFA_OK;
 }
 
@@ -3271,17 +3545,24 @@ int align_launch(const ffa_align_plan* plan, const ffa_align_options* o, const v
                        p.total_slots <= ffa::FUSED_MAX_CHUNKS;
   p.arrivals = !fusable ? nullptr : counters ? counters : arrival_counters(stream);
   const bool fused = p.arrivals != nullptr;
+  BandLaunch band{in[I_BANDS], (size_t)in[I_BAND_LDS], in[I_BAND_BYTES] / 16};
+  if (band.bands > 0) {
+    p.band_ctl = reinterpret_cast<int32_t*>(ws + in[I_WS_BAND]);
+    p.edges = reinterpret_cast<uint64_t*>(
+        ws + in[I_WS_BAND] + align_up(4 * (ffa::BAND_CTL_HEAD + plan->count) + 8 * plan->count, 256));
+    p.band_stride = (int32_t)in[I_BAND_STRIDE];
+  }
   auto run = [&](const auto& tab) -> int {
     using TB = std::decay_t<decltype(tab)>;
     switch (in[I_K]) {
-      case 4: return p.logits ? launch_geometry<4, 8, true, TB>(p, tab, NT, lds, optimized, split, fused, max_frames, stream)
-                              : launch_geometry<4, 8, false, TB>(p, tab, NT, lds, optimized, split, fused, max_frames, stream);
-      case 8: return p.logits ? launch_geometry<8, 6, true, TB>(p, tab, NT, lds, optimized, split, fused, max_frames, stream)
-                              : launch_geometry<8, 6, false, TB>(p, tab, NT, lds, optimized, split, fused, max_frames, stream);
-      case 16: return p.logits ? launch_geometry<16, 4, true, TB>(p, tab, NT, lds, optimized, split, fused, max_frames, stream)
-                               : launch_geometry<16, 4, false, TB>(p, tab, NT, lds, optimized, split, fused, max_frames, stream);
-      case 32: return p.logits ? launch_geometry<32, 1, true, TB>(p, tab, NT, lds, optimized, split, fused, max_frames, stream)
-                               : launch_geometry<32, 1, false, TB>(p, tab, NT, lds, optimized, split, fused, max_frames, stream);
+      case 4: return p.logits ? launch_geometry<4, 8, true, TB>(p, tab, NT, lds, optimized, split, fused, max_frames, band, stream)
+                              : launch_geometry<4, 8, false, TB>(p, tab, NT, lds, optimized, split, fused, max_frames, band, stream);
+      case 8: return p.logits ? launch_geometry<8, 6, true, TB>(p, tab, NT, lds, optimized, split, fused, max_frames, band, stream)
+                              : launch_geometry<8, 6, false, TB>(p, tab, NT, lds, optimized, split, fused, max_frames, band, stream);
+      case 16: return p.logits ? launch_geometry<16, 4, true, TB>(p, tab, NT, lds, optimized, split, fused, max_frames, band, stream)
+                               : launch_geometry<16, 4, false, TB>(p, tab, NT, lds, optimized, split, fused, max_frames, band, stream);
+      case 32: return p.logits ? launch_geometry<32, 1, true, TB>(p, tab, NT, lds, optimized, split, fused, max_frames, band, stream)
+                               : launch_geometry<32, 1, false, TB>(p, tab, NT, lds, optimized, split, fused, max_frames, band, stream);
       default: return fail(FFA_E_INVALID, "corrupt plan");
     }
   };

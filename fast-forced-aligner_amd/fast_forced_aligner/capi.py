@@ -50,7 +50,7 @@ class LogitsRecord(ctypes.Structure):
 class Plan(ctypes.Structure):
     _fields_ = [("count", ctypes.c_int64), ("total_frames", ctypes.c_int64), ("table_bytes", ctypes.c_int64),
                 ("table_uploaded", ctypes.c_int64), ("workspace_bytes", ctypes.c_int64),
-                ("reuse_rows", ctypes.c_int64), ("internal", ctypes.c_int64 * 24)]
+                ("reuse_rows", ctypes.c_int64), ("internal", ctypes.c_int64 * 32)]
 
 
 class Outputs(ctypes.Structure):

@@ -90,7 +90,7 @@ typedef struct ffa_align_plan {
                                the stream reaches the work (pinned memory keeps the copy asynchronous) */
   int64_t workspace_bytes;  /* device scratch for one call (the table's device copy included) */
   int64_t reuse_rows;       /* rows of reuse_stats: B when frontier reuse is active, else 0 */
-  int64_t internal[24];     /* launch geometry; read by ffa_align_launch only */
+  int64_t internal[32];     /* launch geometry; read by ffa_align_launch only */
 } ffa_align_plan;
 
 /* Device output buffers: the ten tensors align() returns, in the order of
