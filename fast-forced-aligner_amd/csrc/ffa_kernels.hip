@@ -1974,6 +1974,14 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) conventional_kernel(Param
 // counts itself on the record's arrival counter with a release; the last band
 // to arrive acquires, selects the terminal state (cu:497-500), walks the path
 // (finish, cu:642-667) and writes the record's outputs.
+//
+// FB (optimized mode, split tail, the same transcripts): the early full
+// fallback of records whose repair budget was exceeded (repair_recurrence,
+// cu:535-550), launched after the tail's first planning pass. Bands of other
+// records return at once. The DP resumes from chunk 0's frontier where it is
+// stored (rows before it are chunk 0's), and the last band leaves the status,
+// objective and reuse counts in the record's tail state with the fallback
+// marked done; repair_kernel's continuation then writes the outputs.
 constexpr int BAND_K = 4;  // a one-wave frame of K = 4 measured 317 ns, of K = 8 362 ns
 constexpr int BAND_STATES = 64 * BAND_K;
 constexpr int BAND_D = 16;                // frames of gathers and edge loads in flight
@@ -2018,8 +2026,9 @@ __device__ inline void conventional_outputs(const Params& p, int rec, int status
   for (int q = 0; q < 3; ++q) { glb(p.shortcut_stats)[3 * rec + q] = 0; glb(p.routing_stats)[3 * rec + q] = 0; }
 }
 
-template <class TB>
+template <class TB, bool FB>
 __global__ void __launch_bounds__(64) band_kernel(Params p, TB tab) {
+  constexpr bool kTab = kArgs<TB> && !FB;  // optimized mode reads the descriptors the chunk kernel left
   extern __shared__ __align__(16) unsigned char lds_raw[];
   const Lds L = carve(lds_raw, p);
   const int lane = threadIdx.x;
@@ -2033,7 +2042,7 @@ __global__ void __launch_bounds__(64) band_kernel(Params p, TB tab) {
     int nb = 0;
     if (i < p.count) {
       int U;
-      if constexpr (kArgs<TB>) U = tab.rec[i].tokens;
+      if constexpr (kTab) U = tab.rec[i].tokens;
       else U = glb(p.desc)[i].tokens;
       nb = (2 * U + 1 + BAND_STATES - 1) / BAND_STATES;
     }
@@ -2050,18 +2059,33 @@ __global__ void __launch_bounds__(64) band_kernel(Params p, TB tab) {
   }
   if (rec < 0) return;  // (the grid has one workgroup per band)
   RecordDesc d;
-  if constexpr (kArgs<TB>) d = tab.rec[rec];
+  if constexpr (kTab) d = tab.rec[rec];
   else d = load_pod(glb(p.desc) + rec);
   Rec r = make_rec(d, p, L);
-  const Staged st = stage_tokens<ALPHABET_NONE>(d, p, rec, L);
   const int S = r.S;
   const int64_t T = r.T;
-  if (st.status >= 2) {  // every band sees the same status; the first writes the outputs (cu:642-652)
-    if (band == 0) {
-      if (lane == 0) conventional_outputs(p, rec, st.status, NEG_INF);
-      write_failed(r, 0, T);
+  int64_t f0 = 0;  // the DP's first column: frame 0, or chunk 0's frontier
+  bool resume = false;
+  int frontier_end = 0;
+  if constexpr (FB) {
+    GLB TailState* state = glb(p.tstate) + rec;
+    const int done = __builtin_amdgcn_readfirstlane(state->done);
+    const int early = __builtin_amdgcn_readfirstlane(state->ts.early);
+    if (done || !(p.overlap && early == 1)) return;  // not an early fallback: nothing to do
+    load_tokens(r, L.ytok);
+    const Slot c0 = load_pod(glb(p.slots) + d.chunk_offset);
+    frontier_end = __builtin_amdgcn_readfirstlane(c0.frontier_end);
+    resume = r.frontier != nullptr && frontier_end > 0 && frontier_end <= T;
+    if (resume) f0 = frontier_end - 1;
+  } else {
+    const Staged st = stage_tokens<ALPHABET_NONE>(d, p, rec, L);
+    if (st.status >= 2) {  // every band sees the same status; the first writes the outputs (cu:642-652)
+      if (band == 0) {
+        if (lane == 0) conventional_outputs(p, rec, st.status, NEG_INF);
+        write_failed(r, 0, T);
+      }
+      return;
     }
-    return;
   }
   constexpr int K = BAND_K;
   const int s0 = band * BAND_STATES + lane * K;
@@ -2087,16 +2111,21 @@ __global__ void __launch_bounds__(64) band_kernel(Params p, TB tab) {
   const GLB uint64_t* ein = band > 0 ? edges + (int64_t)(band - 1) * T : nullptr;
   GLB uint64_t* eout = edges + (int64_t)band * T;  // written only when has_next
   int32_t* ctl = p.band_ctl;
-  // frame 0 (cu:409-410)
+  if (resume) {  // alpha at frame f0 from chunk 0's frontier (cu:451-454)
+    const GLB float* fr = r.frontier;
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const float v = ldg_at(e, lab[k]);
-    al[k] = (s0 + k < S && s0 + k < 2) ? v : NEG_INF;
+    for (int k = 0; k < K; ++k) al[k] = (s0 + k < S) ? fr[s0 + k] : NEG_INF;
+  } else {  // frame 0 (cu:409-410)
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const float v = ldg_at(e, lab[k]);
+      al[k] = (s0 + k < S && s0 + k < 2) ? v : NEG_INF;
+    }
+    if (active) store_row<K>(bp, gtid, 0u);
   }
-  if (active) store_row<K>(bp, gtid, 0u);
   if (has_next && lane == 63)
-    __hip_atomic_store((uint64_t*)eout, (uint64_t)__float_as_uint(al[K - 1]) | (1ull << 32), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store((uint64_t*)(eout + f0), (uint64_t)__float_as_uint(al[K - 1]) | (1ull << 32),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   int late = 0;
   // one frame of the recurrence (cu:438-444); strict '>' keeps stay > advance > skip on ties
   auto frame = [&](int64_t t, const float (&evk)[K], float fill) {
@@ -2121,13 +2150,13 @@ __global__ void __launch_bounds__(64) band_kernel(Params p, TB tab) {
       __hip_atomic_store((uint64_t*)(eout + t), (uint64_t)__float_as_uint(al[K - 1]) | (1ull << 32),
                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
-  if (T > 1) {
+  if (T > f0 + 1) {
     const int64_t last = T - 1;
     float ev[BAND_D][K];
     uint64_t eg[BAND_D];
 #pragma unroll
     for (int dd = 0; dd < BAND_D; ++dd) {
-      const int64_t t = min((int64_t)1 + dd, last);
+      const int64_t t = min(f0 + 1 + dd, last);
       const GLB float* row = e + t * V;
 #pragma unroll
       for (int k = 0; k < K; ++k) ev[dd][k] = ldg_at(row, lab[k]);
@@ -2136,7 +2165,7 @@ __global__ void __launch_bounds__(64) band_kernel(Params p, TB tab) {
     auto fill_of = [&](int dd, int64_t t) -> float {
       return ein ? edge_value(eg[dd], ein + t - 1, late, ctl) : NEG_INF;
     };
-    int64_t t0 = 1;
+    int64_t t0 = f0 + 1;
     for (; t0 + BAND_D <= T; t0 += BAND_D) {
 #pragma unroll
       for (int dd = 0; dd < BAND_D; ++dd) {
@@ -2175,8 +2204,22 @@ __global__ void __launch_bounds__(64) band_kernel(Params p, TB tab) {
   if (S > 1 && v0 >= v1) { terminal = S - 2; score = v0; }
   const bool ok = isfinite(score);
   if (ok) (void)trace_path(r, 0, T, terminal);
-  if (lane == 0) conventional_outputs(p, rec, ok ? 0 : 1, score);  // cu:507-510
-  if (!ok) write_failed(r, 0, T);
+  if constexpr (FB) {  // the tail's continuation writes the outputs (TAIL_RESUME)
+    if (lane == 0) {
+      GLB TailState* state = glb(p.tstate) + rec;
+      state->status = ok ? 0 : 1;
+      state->objective = score;
+      state->ts.early = 2;
+      if (resume && (d.flags & DESC_REUSE_COUNTED)) {
+        unsigned long long* reuse = reinterpret_cast<unsigned long long*>(p.tstate[rec].ts.reuse);
+        atomicAdd(reuse + 1, (unsigned long long)frontier_end);
+        atomicAdd(reuse + 3, (unsigned long long)S);
+      }
+    }
+  } else {
+    if (lane == 0) conventional_outputs(p, rec, ok ? 0 : 1, score);  // cu:507-510
+    if (!ok) write_failed(r, 0, T);
+  }
 }
 
 // Zeroes n 16-byte words (the banded DP's control words and edge arrays).
@@ -2874,13 +2917,14 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) repair_kernel(Params p) {
   if (k >= n) return;
   GLB TailState* state = glb(p.tstate) + rec;
   if (__builtin_amdgcn_readfirstlane(state->done)) return;
-  const int early = __builtin_amdgcn_readfirstlane(state->ts.early);  // 0 or 1 as planned (the fallback writes 2)
+  const int early = __builtin_amdgcn_readfirstlane(state->ts.early);  // 0 or 1 as planned; 2 after band_kernel's fallback
   const int work = __builtin_amdgcn_readfirstlane(state->work);
   GLB Slot* slot = glb(p.slots) + d.chunk_offset + k;
   const Slot s = load_uniform(p.slots + d.chunk_offset + k);
   const bool fallback = p.overlap && early == 1 && k == 0;
+  const bool fell_back = p.overlap && early == 2 && k == 0;  // band_kernel ran the early fallback
   const bool repair = !(p.overlap && early) && s.a < s.b && s.flag;
-  if (!fallback && !repair && !(work == 0 && k == 0)) return;
+  if (!fallback && !fell_back && !repair && !(work == 0 && k == 0)) return;
   Rec r = make_rec(d, p, L);
   if (LG) r.st = p.stats + d.frame_offset;
   load_tokens(r, L.ytok);
@@ -3119,14 +3163,14 @@ int launch_geometry(const ffa::Params& p, const TB& tab, int NT, size_t lds, boo
   if (p.logits && !optimized)
     hipLaunchKernelGGL(ffa::stats_kernel<TB>, dim3((unsigned)((max_frames + 127) / 128), (unsigned)p.count), dim3(256),
                        0, stream, p, tab);
-  if (!optimized && band.bands > 0) {  // zeroed control words and edge arrays, then one workgroup per band
+  if (band.bands > 0) {  // the banded DP's control words and edge arrays start at zero
     const int64_t blocks = std::min<int64_t>(2048, (band.zero_words + 255) / 256);
     hipLaunchKernelGGL(ffa::zero_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
                        reinterpret_cast<ffa::v4i_t*>(p.band_ctl), band.zero_words);
   }
   if (start) (void)hipEventRecord(start, stream);
   if (!optimized && band.bands > 0) {
-    hipLaunchKernelGGL(ffa::band_kernel<TB>, dim3((unsigned)band.bands), dim3(64), band.lds, stream, p, tab);
+    hipLaunchKernelGGL((ffa::band_kernel<TB, false>), dim3((unsigned)band.bands), dim3(64), band.lds, stream, p, tab);
   } else if (!optimized) {
     hipLaunchKernelGGL((ffa::conventional_kernel<K, D, LG, TB>), dim3(p.count), dim3(NT), lds, stream, p, tab);
   } else {
@@ -3150,6 +3194,9 @@ int launch_geometry(const ffa::Params& p, const TB& tab, int NT, size_t lds, boo
     const int64_t n_max = 1 + (max_frames - 1) / p.H;
     q.tail_phase = ffa::TAIL_PLAN0;
     hipLaunchKernelGGL((ffa::tail_kernel<K, D, LG>), dim3(p.count), dim3(NT), lds, stream, q);
+    if (band.bands > 0)  // early full fallbacks as banded DPs
+      hipLaunchKernelGGL((ffa::band_kernel<ffa::NoTable, true>), dim3((unsigned)band.bands), dim3(64), band.lds, stream,
+                         q, ffa::NoTable{0});
     hipLaunchKernelGGL((ffa::repair_kernel<K, D, LG>), dim3((unsigned)n_max, (unsigned)p.count), dim3(NT), lds, stream,
                        q);
   } else if (optimized) {
@@ -3362,12 +3409,13 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
   if (split) ws += align_up((int64_t)sizeof(ffa::TailState) * count, 256);
   const int64_t ws_stats = ws;
   if (logits) ws += align_up(8 * total_frames, 256);
-  // banded DP (conventional mode, log-probabilities, more than 4,096 states):
+  // banded DP (log-probabilities, more than 4,096 states; conventional mode,
+  // or optimized mode's early full fallbacks under the split tail):
   // control words (ticket, late flag, arrival counts, terminal values) and
   // the edge arrays (8 bytes per frame and band boundary of the widest record)
   int64_t bands = 0, band_stride = 0, band_bytes = 0, band_lds = 0;
   const int64_t ws_band = ws;
-  if (!optimized && !logits && K == 32) {
+  if (!logits && K == 32 && (!optimized || split)) {
     int64_t nb_max = 1;
     for (int64_t i = 0; i < count; ++i) {
       const int64_t nb = (states_of(records[i]) + ffa::BAND_STATES - 1) / ffa::BAND_STATES;
