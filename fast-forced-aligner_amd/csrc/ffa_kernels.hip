@@ -1982,9 +1982,9 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) conventional_kernel(Param
 // stored (rows before it are chunk 0's), and the last band leaves the status,
 // objective and reuse counts in the record's tail state with the fallback
 // marked done; repair_kernel's continuation then writes the outputs.
-constexpr int BAND_K = 4;  // a one-wave frame of K = 4 measured 317 ns, of K = 8 362 ns
+constexpr int BAND_K = 4;  // states per lane (C3 conventional: 9.5 ms with K = 4, 10.9 ms with K = 8, same loop)
 constexpr int BAND_STATES = 64 * BAND_K;
-constexpr int BAND_D = 16;                // frames of gathers and edge loads in flight
+constexpr int BAND_D = 8;                 // frames per group of gathers and edge loads in flight (two groups; 16 measured the same)
 constexpr int BAND_SPIN_LIMIT = 1 << 21;  // polls of one entry (about a second) before a band stops waiting
 constexpr int BAND_CTL_HEAD = 64;         // control words: [0] ticket, [1] a wait ran out, then an arrival count per record
 
@@ -2127,6 +2127,13 @@ __global__ void __launch_bounds__(64) band_kernel(Params p, TB tab) {
     __hip_atomic_store((uint64_t*)(eout + f0), (uint64_t)__float_as_uint(al[K - 1]) | (1ull << 32),
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   int late = 0;
+  // Backpointer bytes of this lane (K = 4: one byte per lane and frame),
+  // advanced by one row per frame; lanes past S write into the sink, so the
+  // frame has no exec-masked memory operations and the compiler's waits for
+  // the gathers count the stores exactly.
+  static_assert(K == 4, "one backpointer byte per lane");
+  GLB uint8_t* bpb = active ? (GLB uint8_t*)(bp + (f0 + 1) * stride) + gtid : (GLB uint8_t*)glb(g_bp_sink) + lane;
+  const int64_t bstep = active ? 4 * stride : 0;
   // one frame of the recurrence (cu:438-444); strict '>' keeps stay > advance > skip on ties
   auto frame = [&](int64_t t, const float (&evk)[K], float fill) {
     const float up1 = wave_shr1(al[K - 1], fill);
@@ -2145,42 +2152,52 @@ __global__ void __launch_bounds__(64) band_kernel(Params p, TB tab) {
       al[k] = best + evk[k];
       bits |= j << (2 * k);
     }
-    if (active) store_row<K>(bp + t * stride, gtid, bits);
-    if (has_next && lane == 63)
-      __hip_atomic_store((uint64_t*)(eout + t), (uint64_t)__float_as_uint(al[K - 1]) | (1ull << 32),
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *bpb = (uint8_t)bits;
+    bpb += bstep;
+    if (has_next) {  // every lane stores the last state's value to the same entry
+      const uint32_t v = (uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(al[K - 1]), 63);
+      __hip_atomic_store((uint64_t*)(eout + t), (uint64_t)v | (1ull << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   };
   if (T > f0 + 1) {
     const int64_t last = T - 1;
-    float ev[BAND_D][K];
-    uint64_t eg[BAND_D];
-#pragma unroll
-    for (int dd = 0; dd < BAND_D; ++dd) {
-      const int64_t t = min(f0 + 1 + dd, last);
-      const GLB float* row = e + t * V;
-#pragma unroll
-      for (int k = 0; k < K; ++k) ev[dd][k] = ldg_at(row, lab[k]);
-      eg[dd] = ein ? edge_load(ein + t - 1) : 0ull;
-    }
-    auto fill_of = [&](int dd, int64_t t) -> float {
-      return ein ? edge_value(eg[dd], ein + t - 1, late, ctl) : NEG_INF;
-    };
-    int64_t t0 = f0 + 1;
-    for (; t0 + BAND_D <= T; t0 += BAND_D) {
+    // the first band loads a control word instead (values unused): the loads are unconditional
+    const GLB uint64_t* esrc = ein ? ein : reinterpret_cast<const GLB uint64_t*>(glb(ctl));
+    // Two groups of BAND_D frames in flight: while one group's frames are
+    // computed, the next group's gathers and edge entries load into the other
+    // buffer. The loop body holds both groups, so no loaded value is carried
+    // into the next iteration (a carried ring is copied between registers
+    // there, and the copy waits for the newest loads and write-through stores).
+    float ea[BAND_D][K], eb[BAND_D][K];
+    uint64_t ga[BAND_D], gb[BAND_D];
+    auto load = [&](float (&ev)[BAND_D][K], uint64_t (&eg)[BAND_D], int64_t tg) {
 #pragma unroll
       for (int dd = 0; dd < BAND_D; ++dd) {
-        const int64_t t = t0 + dd;
-        frame(t, ev[dd], fill_of(dd, t));
-        const int64_t tn = min(t + BAND_D, last);
-        const GLB float* row = e + tn * V;
+        const int64_t t = min(tg + dd, last);
+        const GLB float* row = e + t * V;
 #pragma unroll
         for (int k = 0; k < K; ++k) ev[dd][k] = ldg_at(row, lab[k]);
-        if (ein) eg[dd] = edge_load(ein + tn - 1);
+        eg[dd] = edge_load(esrc + (ein ? t - 1 : 0));
       }
-    }
+    };
+    auto run = [&](const float (&ev)[BAND_D][K], const uint64_t (&eg)[BAND_D], int64_t tg, bool whole) {
 #pragma unroll
-    for (int dd = 0; dd < BAND_D; ++dd)
-      if (t0 + dd < T) frame(t0 + dd, ev[dd], fill_of(dd, t0 + dd));
+      for (int dd = 0; dd < BAND_D; ++dd)
+        if (whole || tg + dd < T)
+          frame(tg + dd, ev[dd], ein ? edge_value(eg[dd], ein + tg + dd - 1, late, ctl) : NEG_INF);
+    };
+    int64_t tg = f0 + 1;
+    load(ea, ga, tg);
+    for (;;) {
+      if (tg + BAND_D > T) { run(ea, ga, tg, false); break; }
+      load(eb, gb, tg + BAND_D);
+      run(ea, ga, tg, true);
+      tg += BAND_D;
+      if (tg + BAND_D > T) { run(eb, gb, tg, false); break; }
+      load(ea, ga, tg + BAND_D);
+      run(eb, gb, tg, true);
+      tg += BAND_D;
+    }
   }
   // the terminal candidates S-1 and S-2 (cu:497-500), from whichever band holds them
   GLB float* term = reinterpret_cast<GLB float*>(glb(ctl) + BAND_CTL_HEAD + p.count) + 2 * (int64_t)rec;
