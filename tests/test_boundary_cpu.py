@@ -269,6 +269,29 @@ def test_logits_option_plans_statistics(lib):
     assert rc == -1 and "logits must be 0 or 1" in lib.ffa_last_error().decode()
 
 
+def test_banded_dp_plans_control_words_and_edge_arrays(lib):
+    """Transcripts of more than 4,096 states run the banded DP (bands of 256
+    states) in conventional mode and, under the split tail, for optimized
+    mode's early fallbacks; log-probability input only. The plan adds control
+    words (64 + B ints and two floats per record, 256-byte aligned) and 8 bytes
+    per frame and band boundary of the widest record to the workspace."""
+    wide = [(3000, 32, 2200, 0), (500, 32, 100, 0)]   # S = 4401 (18 bands) and 201 (1 band)
+    band = -(-(-(-(4 * (64 + 2) + 8 * 2) // 256) * 256 + 8 * 3500 * 17) // 256) * 256
+    stats = -(-8 * 3500 // 256) * 256
+    rc, conv, _ = _plan(lib, wide, optimized=False)
+    rc2, conv_lg, _ = _plan(lib, wide, optimized=False, logits=1)   # logits keep the one-workgroup DP
+    assert rc == 0 and rc2 == 0
+    assert conv.workspace_bytes - conv_lg.workspace_bytes == band - stats
+    rc, opt, _ = _plan(lib, wide)                     # T_max >= 2048: split tail, banded early fallbacks
+    rc2, opt_r0, _ = _plan(lib, wide, repair_rounds=0)  # no split tail, no banded DP
+    assert rc == 0 and rc2 == 0
+    assert opt.workspace_bytes - opt_r0.workspace_bytes == 256 + band  # + one 112-byte tail state per record
+    narrow = [(3000, 32, 2000, 0), (500, 32, 100, 0)]  # S = 4001: K = 16, one workgroup per record
+    rc, conv, _ = _plan(lib, narrow, optimized=False)
+    rc2, conv_lg, _ = _plan(lib, narrow, optimized=False, logits=1)
+    assert rc == 0 and rc2 == 0 and conv_lg.workspace_bytes - conv.workspace_bytes == stats
+
+
 def test_logits_entry_points_check_arguments_on_the_host(lib):
     assert lib.ffa_log_softmax_launch(None, 1, 10, None) == -1
     assert "null record" in lib.ffa_last_error().decode()

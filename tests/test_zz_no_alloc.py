@@ -1,10 +1,13 @@
 """The allocation-free entry point (ffa_align_launch_noalloc): its outputs
 equal ffa_align_launch's bit for bit, on calls in a row whose later batches
 are smaller (the shared device array keeps the first call's contents): a
-1,024-record batch (chunk and tail kernels), then two batches that run as one
-launch with the fused tail, whose arrival counters live in a second fixed
-array (12 C2 records, then C1, whose records are repaired); and a batch beyond
-its fixed scratch is refused."""
+1,024-record batch (chunk and tail kernels), then a batch with a transcript of
+more than 4,096 states (the banded DP, whose control words and edge arrays sit
+in the fixed array too; near-flat rows, so that optimized mode sends it to the
+early full fallback), then two batches that run as one launch with the fused
+tail, whose arrival counters live in a second fixed array (12 C2 records, then
+C1, whose records are repaired); and a batch beyond its fixed scratch is
+refused."""
 from __future__ import annotations
 
 import ctypes
@@ -75,12 +78,20 @@ def test_noalloc_matches_launch_on_two_calls(optimized):
     big = _device(workloads.make("c5"))        # 1,024 records: ~11 MiB of scratch
     small = _device(workloads.c2(batch=12))    # then a smaller batch over the stale contents
     tiny = _device(workloads.c1())             # fused tail with repairs, counters left by the last call
-    for name, (es, ys) in (("c5", big), ("c2x12", small), ("c1", tiny)):
+    rng = np.random.default_rng(2100)
+    y = rng.integers(1, 32, size=2100).astype(np.int64)
+    flat = workloads._log_softmax((0.01 * rng.standard_normal((2300, 32))).astype(np.float32))
+    y2 = rng.integers(1, 32, size=100).astype(np.int64)
+    wide = ([torch.from_numpy(flat).to(DEV), torch.from_numpy(workloads.peaky(rng, y2, 600, 32)).to(DEV)],
+            [torch.from_numpy(y).to(DEV), torch.from_numpy(y2).to(DEV)])  # S = 4201: 17 bands
+    for name, (es, ys) in (("c5", big), ("wide", wide), ("c2x12", small), ("c1", tiny)):
         print(f"noalloc {name} optimized={optimized}", flush=True)
         want = _run(lib, es, ys, optimized, noalloc=False)
         got = _run(lib, es, ys, optimized, noalloc=True)
         assert_same(got, want, where=f"noalloc {name} ")
         assert not (got["labels"] == -7).all()
+        if name == "wide" and optimized:
+            assert want["routing_stats"][0, 0] == 2  # the early full fallback ran (banded)
 
 
 def test_noalloc_rejects_batches_beyond_its_scratch():
