@@ -449,10 +449,10 @@ def main() -> int:
         achieved = min_bytes / (kernel_ms * 1e-3) / 1e9
         return step_s, kernel_ms, achieved, result
 
-    # conventional mode cuts transcripts of more than 4,096 states into bands of
+    # conventional mode cuts transcripts of more than 1,024 states into bands of
     # 256 states, one single-wave workgroup each (band_kernel, ffa_kernels.hip)
     states = [2 * len(y) + 1 for y in batch.targets]
-    banded = args.mode == "conventional" and max(states) > 4096
+    banded = args.mode == "conventional" and max(states) > 1024
     kernel_name = "chunk_kernel" if args.mode == "optimized" else "band_kernel" if banded else "conventional_kernel"
     # optimized mode runs each record's tail inside the chunk kernel (one launch
     # per call) for batches of log-probabilities with at most 1,024 chunks, at

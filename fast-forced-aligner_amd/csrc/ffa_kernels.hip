@@ -1953,7 +1953,7 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) conventional_kernel(Param
 }
 
 // ---------------------------------------------------------------------------
-// Banded DP: conventional mode for batches with transcripts of more than 4,096
+// Banded DP: conventional mode for batches with transcripts of more than 1,024
 // states. A record's states are cut into bands of BAND_STATES, one wave each
 // (BAND_K contiguous states per lane), and every band is a workgroup of its
 // own, so a record of 18,001 states runs on 71 CUs instead of one. State s at
@@ -3164,7 +3164,7 @@ enum {
 };
 static_assert(I_BAND_LDS < 32, "plan->internal holds 32 values");
 
-// Banded DP launch (conventional mode, transcripts of more than 4,096 states):
+// Banded DP launch (conventional mode, transcripts of more than 1,024 states):
 // workgroups (one per band), LDS bytes, and the 16-byte words zeroed first.
 struct BandLaunch {
   int64_t bands;
@@ -3426,13 +3426,13 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
   if (split) ws += align_up((int64_t)sizeof(ffa::TailState) * count, 256);
   const int64_t ws_stats = ws;
   if (logits) ws += align_up(8 * total_frames, 256);
-  // banded DP (log-probabilities, more than 4,096 states; conventional mode,
+  // banded DP (log-probabilities, more than 1,024 states; conventional mode,
   // or optimized mode's early full fallbacks under the split tail):
   // control words (ticket, late flag, arrival counts, terminal values) and
   // the edge arrays (8 bytes per frame and band boundary of the widest record)
   int64_t bands = 0, band_stride = 0, band_bytes = 0, band_lds = 0;
   const int64_t ws_band = ws;
-  if (!logits && K == 32 && (!optimized || split)) {
+  if (!logits && K >= 8 && (!optimized || split)) {
     int64_t nb_max = 1;
     for (int64_t i = 0; i < count; ++i) {
       const int64_t nb = (states_of(records[i]) + ffa::BAND_STATES - 1) / ffa::BAND_STATES;

@@ -270,7 +270,7 @@ def test_logits_option_plans_statistics(lib):
 
 
 def test_banded_dp_plans_control_words_and_edge_arrays(lib):
-    """Transcripts of more than 4,096 states run the banded DP (bands of 256
+    """Transcripts of more than 1,024 states run the banded DP (bands of 256
     states) in conventional mode and, under the split tail, for optimized
     mode's early fallbacks; log-probability input only. The plan adds control
     words (64 + B ints and two floats per record, 256-byte aligned) and 8 bytes
@@ -286,7 +286,7 @@ def test_banded_dp_plans_control_words_and_edge_arrays(lib):
     rc2, opt_r0, _ = _plan(lib, wide, repair_rounds=0)  # no split tail, no banded DP
     assert rc == 0 and rc2 == 0
     assert opt.workspace_bytes - opt_r0.workspace_bytes == 256 + band  # + one 112-byte tail state per record
-    narrow = [(3000, 32, 2000, 0), (500, 32, 100, 0)]  # S = 4001: K = 16, one workgroup per record
+    narrow = [(3000, 32, 500, 0), (500, 32, 100, 0)]  # S = 1001: K = 4, one workgroup per record
     rc, conv, _ = _plan(lib, narrow, optimized=False)
     rc2, conv_lg, _ = _plan(lib, narrow, optimized=False, logits=1)
     assert rc == 0 and rc2 == 0 and conv_lg.workspace_bytes - conv.workspace_bytes == stats

@@ -1,5 +1,5 @@
 """GPU parity for the banded DP: conventional mode on batches with transcripts
-of more than 4,096 states, where every record's states are cut into bands of
+of more than 1,024 states, where every record's states are cut into bands of
 256 (one wave each) that run as workgroups of their own and hand the last
 state of each frame to the next band through global memory.
 

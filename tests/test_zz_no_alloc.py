@@ -2,7 +2,7 @@
 equal ffa_align_launch's bit for bit, on calls in a row whose later batches
 are smaller (the shared device array keeps the first call's contents): a
 1,024-record batch (chunk and tail kernels), then a batch with a transcript of
-more than 4,096 states (the banded DP, whose control words and edge arrays sit
+more than 1,024 states (the banded DP, whose control words and edge arrays sit
 in the fixed array too; near-flat rows, so that optimized mode sends it to the
 early full fallback), then two batches that run as one launch with the fused
 tail, whose arrival counters live in a second fixed array (12 C2 records, then
