@@ -2170,14 +2170,33 @@ __global__ void __launch_bounds__(64) band_kernel(Params p, TB tab) {
     // there, and the copy waits for the newest loads and write-through stores).
     float ea[BAND_D][K], eb[BAND_D][K];
     uint64_t ga[BAND_D], gb[BAND_D];
+    // A group inside the record gathers from one row base with per-lane
+    // offsets fixed for the whole loop (no per-frame clamp or 64-bit product
+    // in scalar registers); the record's last groups clamp every frame.
+    uint32_t off[BAND_D][K];
+#pragma unroll
+    for (int dd = 0; dd < BAND_D; ++dd)
+#pragma unroll
+      for (int k = 0; k < K; ++k) off[dd][k] = lab[k] + (uint32_t)(4 * dd) * (uint32_t)V;
     auto load = [&](float (&ev)[BAND_D][K], uint64_t (&eg)[BAND_D], int64_t tg) {
+      if (tg + BAND_D - 1 <= last) {
+        const GLB float* row0 = e + tg * V;
+        const GLB uint64_t* e0 = esrc + (ein ? tg - 1 : 0);
 #pragma unroll
-      for (int dd = 0; dd < BAND_D; ++dd) {
-        const int64_t t = min(tg + dd, last);
-        const GLB float* row = e + t * V;
+        for (int dd = 0; dd < BAND_D; ++dd) {
 #pragma unroll
-        for (int k = 0; k < K; ++k) ev[dd][k] = ldg_at(row, lab[k]);
-        eg[dd] = edge_load(esrc + (ein ? t - 1 : 0));
+          for (int k = 0; k < K; ++k) ev[dd][k] = ldg_at(row0, off[dd][k]);
+          eg[dd] = edge_load(e0 + (ein ? dd : 0));
+        }
+      } else {
+#pragma unroll
+        for (int dd = 0; dd < BAND_D; ++dd) {
+          const int64_t t = min(tg + dd, last);
+          const GLB float* row = e + t * V;
+#pragma unroll
+          for (int k = 0; k < K; ++k) ev[dd][k] = ldg_at(row, lab[k]);
+          eg[dd] = edge_load(esrc + (ein ? t - 1 : 0));
+        }
       }
     };
     auto run = [&](const float (&ev)[BAND_D][K], const uint64_t (&eg)[BAND_D], int64_t tg, bool whole) {
