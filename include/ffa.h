@@ -134,7 +134,12 @@ int ffa_align_describe(const ffa_align_plan* plan, const ffa_record* records,
  * 128 KiB of arrival counters per (device, stream) (one per 128-byte line for
  * up to 1,024 records), allocated and zeroed on the stream's first such call
  * and kept until the process ends.
- * A stream under graph capture that has none yet takes the two-launch form. */
+ * A stream under graph capture that has none yet takes the two-launch form.
+ * Batches of log-probabilities with a transcript of more than 1,024 states
+ * (conventional mode, or optimized mode with a record of 2,048+ frames) run
+ * the full DP in bands of 256 states, one workgroup each; the launch first
+ * zeroes the bands' control words and edge arrays, which the plan places in
+ * the workspace (no kernel of this entry writes memory it does not own). */
 int ffa_align_launch(const ffa_align_plan* plan, const ffa_align_options* options,
                      const void* host_table, const uint8_t* emission_validity,
                      const ffa_align_outputs* outputs, void* workspace, hipStream_t stream);
