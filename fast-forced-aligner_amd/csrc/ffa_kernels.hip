@@ -1962,13 +1962,15 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) conventional_kernel(Param
 // needs from outside is the previous band's last state at frame t-1. Band j
 // publishes that value for every frame as one 8-byte entry of its edge array
 // (the float and a valid tag, an agent-scope store written through to
-// memory); band j+1 loads the entry BAND_D frames ahead with an agent-scope
-// load and checks the tag at use, so it runs a few frames behind band j. The
+// memory); band j+1 loads the entries a group of BAND_D frames ahead with
+// agent-scope loads and checks each tag at use, so it runs a few frames behind
+// band j. The
 // edge arrays and control words are zeroed before each call (zero_kernel).
 // Workgroups take their band from a ticket counter in the order they start,
 // so band j-1 is running whenever band j waits for it and every wait ends;
 // a wait is bounded all the same (BAND_SPIN_LIMIT polls of one entry, then
-// the band waits no more, uses NaN and flags the call in control word 1).
+// the band waits no more and uses NaN, so a broken hand-off gives wrong
+// results instead of a hang, and sets control word 1 in the workspace).
 // Each band writes its lanes' part of every backpointer row (the layout of
 // the one-workgroup DP: thread index band*64+lane with BAND_K states), then
 // counts itself on the record's arrival counter with a release; the last band
