@@ -1924,6 +1924,16 @@ __device__ __attribute__((always_inline)) int greedy_fast(const Lds& L, const fl
 // ---------------------------------------------------------------------------
 // Kernels.
 
+// The per-record outputs of conventional mode besides the path.
+__device__ inline void conventional_outputs(const Params& p, int rec, int status, float objective) {
+  glb(p.status)[rec] = status;
+  glb(p.objective)[rec] = objective;
+  glb(p.stitched)[rec] = 0;
+  glb(p.repair_passes)[rec] = 0;
+  glb(p.repaired_frames)[rec] = 0;
+  for (int q = 0; q < 3; ++q) { glb(p.shortcut_stats)[3 * rec + q] = 0; glb(p.routing_stats)[3 * rec + q] = 0; }
+}
+
 template <int K, int D, bool LG, class TB>
 __global__ void __launch_bounds__(K == 32 ? 640 : 256) conventional_kernel(Params p, TB tab) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
@@ -1935,20 +1945,14 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) conventional_kernel(Param
   Rec r = make_rec(d, p, L);
   if (LG) r.st = p.stats + d.frame_offset;
   const Staged st = stage_tokens<ALPHABET_NONE>(d, p, rec, L);
-  if (threadIdx.x == 0) {
-    glb(p.stitched)[rec] = 0;
-    glb(p.repair_passes)[rec] = 0;
-    glb(p.repaired_frames)[rec] = 0;
-    for (int q = 0; q < 3; ++q) { glb(p.shortcut_stats)[3 * rec + q] = 0; glb(p.routing_stats)[3 * rec + q] = 0; }
-  }
   if (st.status >= 2) {
-    if (threadIdx.x == 0) { glb(p.status)[rec] = st.status; glb(p.objective)[rec] = NEG_INF; }
+    if (threadIdx.x == 0) conventional_outputs(p, rec, st.status, NEG_INF);
     write_failed(r, 0, r.T);
     return;
   }
   const DPOut o = dp_interval<K, D, LG, false>(r, L, 0, r.T, true, nullptr, 1, nullptr, TRACE_IF_FINITE);
   const bool ok = isfinite(o.score);
-  if (threadIdx.x == 0) { glb(p.status)[rec] = ok ? 0 : 1; glb(p.objective)[rec] = o.score; }  // cu:507-510
+  if (threadIdx.x == 0) conventional_outputs(p, rec, ok ? 0 : 1, o.score);  // cu:507-510
   if (!ok) write_failed(r, 0, r.T);
 }
 
@@ -2016,16 +2020,6 @@ __device__ inline float edge_value(uint64_t ent, const GLB uint64_t* at, int& la
     }
   }
   return __uint_as_float(val);
-}
-
-// The per-record outputs of conventional mode besides the path.
-__device__ inline void conventional_outputs(const Params& p, int rec, int status, float objective) {
-  glb(p.status)[rec] = status;
-  glb(p.objective)[rec] = objective;
-  glb(p.stitched)[rec] = 0;
-  glb(p.repair_passes)[rec] = 0;
-  glb(p.repaired_frames)[rec] = 0;
-  for (int q = 0; q < 3; ++q) { glb(p.shortcut_stats)[3 * rec + q] = 0; glb(p.routing_stats)[3 * rec + q] = 0; }
 }
 
 template <class TB, bool FB>
