@@ -122,6 +122,9 @@ SPLIT_KNOBS = {
     "chunk256": dict(chunk_frames=256),
     "mode1": dict(mode=1),
     "repair_threads128": dict(repair_threads=128, threads=128),
+    # no stored frontier (chunks under 32 frames, frontier reuse off): the
+    # banded early fallback starts at frame 0
+    "chunk16_frontier_off": dict(chunk_frames=16, frontier_reuse=False),
 }
 
 
@@ -133,3 +136,5 @@ def test_knobs_on_the_split_path(family):
     got, want = _run(es, ys, knobs)
     assert_same(got, want, where=f"split {family} ")
     assert (got["repair_passes"] > 0).any()
+    if family == "chunk16_frontier_off":
+        assert 2 in got["routing_stats"][:, 0].tolist()  # an early fallback ran, from frame 0
