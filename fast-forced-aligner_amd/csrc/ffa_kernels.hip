@@ -175,7 +175,9 @@ struct TailState {
   float objective;  // after an early full fallback
   int32_t work;     // first-round DPs planned for the record (repair intervals or the early fallback)
   int32_t pending;  // of those, not finished yet
-  int32_t pad[3];
+  int32_t fallback;       // the seams failed: band_kernel runs the full fallback and writes the outputs
+  int32_t fallback_from;  // chunk 0's frontier end for that fallback (0: none)
+  int32_t pad;
 };
 static_assert(sizeof(TailState) % 16 == 0, "16-byte granules");
 
@@ -1924,6 +1926,26 @@ __device__ __attribute__((always_inline)) int greedy_fast(const Lds& L, const fl
 // ---------------------------------------------------------------------------
 // Kernels.
 
+// The per-record outputs of optimized mode besides the path (thread 0).
+__device__ inline void tail_outputs(const Params& p, int rec, const TailStats& ts, int status, float objective,
+                                    int stitched) {
+  glb(p.status)[rec] = status;
+  glb(p.objective)[rec] = objective;
+  glb(p.stitched)[rec] = stitched;
+  glb(p.repair_passes)[rec] = ts.passes;
+  glb(p.repaired_frames)[rec] = ts.repaired;
+  glb(p.shortcut_stats)[3 * rec + 0] = ts.sc_accepted;
+  glb(p.shortcut_stats)[3 * rec + 1] = ts.sc_frames;
+  glb(p.shortcut_stats)[3 * rec + 2] = ts.sc_ambiguous;
+  glb(p.routing_stats)[3 * rec + 0] = ts.early;
+  glb(p.routing_stats)[3 * rec + 1] = ts.rejected;
+  glb(p.routing_stats)[3 * rec + 2] = ts.maxprop;
+  if (p.reuse_stats) {
+    GLB int64_t* u = glb(p.reuse_stats) + 4 * rec;
+    u[0] = ts.reuse[0]; u[1] = ts.reuse[1]; u[2] = ts.reuse[2]; u[3] = ts.reuse[3];
+  }
+}
+
 // The per-record outputs of conventional mode besides the path.
 __device__ inline void conventional_outputs(const Params& p, int rec, int status, float objective) {
   glb(p.status)[rec] = status;
@@ -1992,7 +2014,8 @@ constexpr int BAND_K = 4;  // states per lane (C3 conventional: 9.5 ms with K = 
 constexpr int BAND_STATES = 64 * BAND_K;
 constexpr int BAND_D = 8;                 // frames per group of gathers and edge loads in flight (two groups; 16 measured the same)
 constexpr int BAND_SPIN_LIMIT = 1 << 21;  // polls of one entry (about a second) before a band stops waiting
-constexpr int BAND_CTL_HEAD = 64;         // control words: [0] ticket, [1] a wait ran out, then an arrival count per record
+constexpr int BAND_CTL_HEAD = 64;         // control words: [0] ticket, [1] a wait ran out, [2] ticket of the fallback after
+                                          // failed seams, then an arrival count per record
 
 __device__ inline uint64_t edge_load(const GLB uint64_t* at) {
   return __hip_atomic_load((const uint64_t*)at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -2022,14 +2045,15 @@ __device__ inline float edge_value(uint64_t ent, const GLB uint64_t* at, int& la
   return __uint_as_float(val);
 }
 
-template <class TB, bool FB>
+template <class TB, int FB>
 __global__ void __launch_bounds__(64) band_kernel(Params p, TB tab) {
-  constexpr bool kTab = kArgs<TB> && !FB;  // optimized mode reads the descriptors the chunk kernel left
+  constexpr bool kTab = kArgs<TB> && FB == 0;  // optimized mode reads the descriptors the chunk kernel left
   extern __shared__ __align__(16) unsigned char lds_raw[];
   const Lds L = carve(lds_raw, p);
   const int lane = threadIdx.x;
   int ticket = 0;
-  if (lane == 0) ticket = __hip_atomic_fetch_add(p.band_ctl, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (lane == 0)  // the fallback after failed seams counts on its own ticket word
+    ticket = __hip_atomic_fetch_add(p.band_ctl + (FB == 2 ? 2 : 0), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   ticket = __builtin_amdgcn_readlane(ticket, 0);
   // ticket -> (record, band): bands are numbered record by record
   int rec = -1, band = 0, bands = 1;
@@ -2063,14 +2087,19 @@ __global__ void __launch_bounds__(64) band_kernel(Params p, TB tab) {
   int64_t f0 = 0;  // the DP's first column: frame 0, or chunk 0's frontier
   bool resume = false;
   int frontier_end = 0;
-  if constexpr (FB) {
+  if constexpr (FB != 0) {
     GLB TailState* state = glb(p.tstate) + rec;
     const int done = __builtin_amdgcn_readfirstlane(state->done);
-    const int early = __builtin_amdgcn_readfirstlane(state->ts.early);
-    if (done || !(p.overlap && early == 1)) return;  // not an early fallback: nothing to do
+    if constexpr (FB == 1) {
+      const int early = __builtin_amdgcn_readfirstlane(state->ts.early);
+      if (done || !(p.overlap && early == 1)) return;  // not an early fallback: nothing to do
+      const Slot c0 = load_pod(glb(p.slots) + d.chunk_offset);
+      frontier_end = __builtin_amdgcn_readfirstlane(c0.frontier_end);
+    } else {
+      if (done || !__builtin_amdgcn_readfirstlane(state->fallback)) return;  // stitched, or finished before
+      frontier_end = __builtin_amdgcn_readfirstlane(state->fallback_from);
+    }
     load_tokens(r, L.ytok);
-    const Slot c0 = load_pod(glb(p.slots) + d.chunk_offset);
-    frontier_end = __builtin_amdgcn_readfirstlane(c0.frontier_end);
     resume = r.frontier != nullptr && frontier_end > 0 && frontier_end <= T;
     if (resume) f0 = frontier_end - 1;
   } else {
@@ -2166,33 +2195,14 @@ __global__ void __launch_bounds__(64) band_kernel(Params p, TB tab) {
     // there, and the copy waits for the newest loads and write-through stores).
     float ea[BAND_D][K], eb[BAND_D][K];
     uint64_t ga[BAND_D], gb[BAND_D];
-    // A group inside the record gathers from one row base with per-lane
-    // offsets fixed for the whole loop (no per-frame clamp or 64-bit product
-    // in scalar registers); the record's last groups clamp every frame.
-    uint32_t off[BAND_D][K];
-#pragma unroll
-    for (int dd = 0; dd < BAND_D; ++dd)
-#pragma unroll
-      for (int k = 0; k < K; ++k) off[dd][k] = lab[k] + (uint32_t)(4 * dd) * (uint32_t)V;
     auto load = [&](float (&ev)[BAND_D][K], uint64_t (&eg)[BAND_D], int64_t tg) {
-      if (tg + BAND_D - 1 <= last) {
-        const GLB float* row0 = e + tg * V;
-        const GLB uint64_t* e0 = esrc + (ein ? tg - 1 : 0);
 #pragma unroll
-        for (int dd = 0; dd < BAND_D; ++dd) {
+      for (int dd = 0; dd < BAND_D; ++dd) {
+        const int64_t t = min(tg + dd, last);
+        const GLB float* row = e + t * V;
 #pragma unroll
-          for (int k = 0; k < K; ++k) ev[dd][k] = ldg_at(row0, off[dd][k]);
-          eg[dd] = edge_load(e0 + (ein ? dd : 0));
-        }
-      } else {
-#pragma unroll
-        for (int dd = 0; dd < BAND_D; ++dd) {
-          const int64_t t = min(tg + dd, last);
-          const GLB float* row = e + t * V;
-#pragma unroll
-          for (int k = 0; k < K; ++k) ev[dd][k] = ldg_at(row, lab[k]);
-          eg[dd] = edge_load(esrc + (ein ? t - 1 : 0));
-        }
+        for (int k = 0; k < K; ++k) ev[dd][k] = ldg_at(row, lab[k]);
+        eg[dd] = edge_load(esrc + (ein ? t - 1 : 0));
       }
     };
     auto run = [&](const float (&ev)[BAND_D][K], const uint64_t (&eg)[BAND_D], int64_t tg, bool whole) {
@@ -2236,7 +2246,14 @@ __global__ void __launch_bounds__(64) band_kernel(Params p, TB tab) {
   if (S > 1 && v0 >= v1) { terminal = S - 2; score = v0; }
   const bool ok = isfinite(score);
   if (ok) (void)trace_path(r, 0, T, terminal);
-  if constexpr (FB) {  // the tail's continuation writes the outputs (TAIL_RESUME)
+  if constexpr (FB == 2) {  // fallback_recurrence after failed seams (cu:552-559): the record's outputs
+    if (!ok) write_failed(r, 0, T);
+    if (lane == 0) {
+      TailStats ts = load_pod(&glb(p.tstate)[rec].ts);
+      if (resume && (d.flags & DESC_REUSE_COUNTED)) { ts.reuse[1] += frontier_end; ts.reuse[3] += S; }
+      tail_outputs(p, rec, ts, ok ? 0 : 1, score, 0);
+    }
+  } else if constexpr (FB == 1) {  // the tail's continuation writes the outputs (TAIL_RESUME)
     if (lane == 0) {
       GLB TailState* state = glb(p.tstate) + rec;
       state->status = ok ? 0 : 1;
@@ -2539,6 +2556,7 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
         for (int k = 0; k < n; ++k) work += sl[k].a < sl[k].b && sl[k].flag;
       store_pod(&state->ts, ts);
       state->done = 0;
+      state->fallback = 0;
       state->status = 0;
       state->objective = NEG_INF;
       state->work = work;
@@ -2570,6 +2588,14 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
     status = 0;
     objective = h->fbuf[2];
     __syncthreads();
+    if (!stitched && phase == TAIL_RESUME && p.band_ctl) {  // banded: band_kernel<.., 2> runs it and writes the outputs
+      if (tid == 0) {
+        store_pod(&state->ts, ts);
+        state->fallback_from = load_slot(sl + (0)).frontier_end;
+        state->fallback = 1;
+      }
+      return;
+    }
     if (!stitched) {  // fallback_recurrence, cu:552-559
       const Slot s0 = load_slot(sl + (0));
       const bool resume = frontier_on && s0.frontier_end > 0 && s0.frontier_end <= T;
@@ -2581,23 +2607,7 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
     }
   }
   if (status != 0) write_failed(r, 0, T);
-  if (tid == 0) {
-    glb(p.status)[rec] = status;
-    glb(p.objective)[rec] = objective;
-    glb(p.stitched)[rec] = stitched;
-    glb(p.repair_passes)[rec] = ts.passes;
-    glb(p.repaired_frames)[rec] = ts.repaired;
-    glb(p.shortcut_stats)[3 * rec + 0] = ts.sc_accepted;
-    glb(p.shortcut_stats)[3 * rec + 1] = ts.sc_frames;
-    glb(p.shortcut_stats)[3 * rec + 2] = ts.sc_ambiguous;
-    glb(p.routing_stats)[3 * rec + 0] = ts.early;
-    glb(p.routing_stats)[3 * rec + 1] = ts.rejected;
-    glb(p.routing_stats)[3 * rec + 2] = ts.maxprop;
-    if (p.reuse_stats) {
-      GLB int64_t* u = glb(p.reuse_stats) + 4 * rec;
-      u[0] = ts.reuse[0]; u[1] = ts.reuse[1]; u[2] = ts.reuse[2]; u[3] = ts.reuse[3];
-    }
-  }
+  if (tid == 0) tail_outputs(p, rec, ts, status, objective, stitched);
 }
 
 // Fast path of one record's tail in wave 0 (tid < 64, n <= 64 chunks): a
@@ -3202,7 +3212,7 @@ int launch_geometry(const ffa::Params& p, const TB& tab, int NT, size_t lds, boo
   }
   if (start) (void)hipEventRecord(start, stream);
   if (!optimized && band.bands > 0) {
-    hipLaunchKernelGGL((ffa::band_kernel<TB, false>), dim3((unsigned)band.bands), dim3(64), band.lds, stream, p, tab);
+    hipLaunchKernelGGL((ffa::band_kernel<TB, 0>), dim3((unsigned)band.bands), dim3(64), band.lds, stream, p, tab);
   } else if (!optimized) {
     hipLaunchKernelGGL((ffa::conventional_kernel<K, D, LG, TB>), dim3(p.count), dim3(NT), lds, stream, p, tab);
   } else {
@@ -3227,10 +3237,13 @@ int launch_geometry(const ffa::Params& p, const TB& tab, int NT, size_t lds, boo
     q.tail_phase = ffa::TAIL_PLAN0;
     hipLaunchKernelGGL((ffa::tail_kernel<K, D, LG>), dim3(p.count), dim3(NT), lds, stream, q);
     if (band.bands > 0)  // early full fallbacks as banded DPs
-      hipLaunchKernelGGL((ffa::band_kernel<ffa::NoTable, true>), dim3((unsigned)band.bands), dim3(64), band.lds, stream,
+      hipLaunchKernelGGL((ffa::band_kernel<ffa::NoTable, 1>), dim3((unsigned)band.bands), dim3(64), band.lds, stream,
                          q, ffa::NoTable{0});
     hipLaunchKernelGGL((ffa::repair_kernel<K, D, LG>), dim3((unsigned)n_max, (unsigned)p.count), dim3(NT), lds, stream,
                        q);
+    if (band.bands > 0)  // fallbacks after failed seams as banded DPs
+      hipLaunchKernelGGL((ffa::band_kernel<ffa::NoTable, 2>), dim3((unsigned)band.bands), dim3(64), band.lds, stream,
+                         q, ffa::NoTable{0});
   } else if (optimized) {
     hipLaunchKernelGGL((ffa::tail_kernel<K, D, LG>), dim3(p.count), dim3(NT), lds, stream, p);
   }
