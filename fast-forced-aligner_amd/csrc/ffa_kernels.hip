@@ -2349,7 +2349,7 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
   const int64_t T = r.T;
   const int n = (int)(1 + (T - 1) / p.H);
   const bool split = phase != TAIL_ALL;
-  GLB TailState* state = split ? glb(p.tstate) + rec : nullptr;
+  GLB TailState* state = p.tstate ? glb(p.tstate) + rec : nullptr;  // split tail, or banded fallbacks
   const int status0 = sl[0].status;
   if (status0 >= 2 && (!split || phase == TAIL_PLAN0)) {
     if (tid == 0) {
@@ -2588,7 +2588,7 @@ __device__ __attribute__((always_inline)) void tail_body(const Params& p, const 
     status = 0;
     objective = h->fbuf[2];
     __syncthreads();
-    if (!stitched && phase == TAIL_RESUME && p.band_ctl) {  // banded: band_kernel<.., 2> runs it and writes the outputs
+    if (!stitched && p.band_ctl && state) {  // banded: band_kernel<.., 2> runs it and writes the outputs
       if (tid == 0) {
         store_pod(&state->ts, ts);
         state->fallback_from = load_slot(sl + (0)).frontier_end;
@@ -2923,6 +2923,10 @@ __global__ void __launch_bounds__(K == 32 ? 640 : 256) tail_kernel(Params p) {
   const RecordDesc d = load_uniform(p.desc + rec);
   const int n = (int)(1 + (d.frames - 1) / p.H);
   const bool split = p.tail_phase != TAIL_ALL;
+  if (!split && p.tstate && tid == 0) {  // one-pass tail with banded fallbacks: none handed over yet
+    glb(p.tstate)[rec].done = 0;
+    glb(p.tstate)[rec].fallback = 0;
+  }
   if (n <= 64) {
     if (tid < 64) {
       const int done = tail_fast<false>(p, d, rec, glb(p.slots) + d.chunk_offset, n);
@@ -3246,6 +3250,9 @@ int launch_geometry(const ffa::Params& p, const TB& tab, int NT, size_t lds, boo
                          q, ffa::NoTable{0});
   } else if (optimized) {
     hipLaunchKernelGGL((ffa::tail_kernel<K, D, LG>), dim3(p.count), dim3(NT), lds, stream, p);
+    if (band.bands > 0)  // fallbacks after failed seams as banded DPs
+      hipLaunchKernelGGL((ffa::band_kernel<ffa::NoTable, 2>), dim3((unsigned)band.bands), dim3(64), band.lds, stream,
+                         p, ffa::NoTable{0});
   }
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(FFA_E_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
@@ -3450,8 +3457,12 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
   // round's intervals in parallel workgroups (a few more launches, against
   // repair DPs of milliseconds)
   const bool split = optimized && o->repair_rounds > 0 && max_frames >= 2048 && count * n_max <= (1 << 20);
+  // optimized batches of transcripts with more than 4,096 states that take no
+  // split tail (no repair rounds) hand their fallbacks to the banded DP too,
+  // through the same per-record state
+  const bool band_tail = optimized && !split && !logits && K == 32;
   const int64_t ws_tstate = ws;
-  if (split) ws += align_up((int64_t)sizeof(ffa::TailState) * count, 256);
+  if (split || band_tail) ws += align_up((int64_t)sizeof(ffa::TailState) * count, 256);
   const int64_t ws_stats = ws;
   if (logits) ws += align_up(8 * total_frames, 256);
   // banded DP (log-probabilities, more than 1,024 states; conventional mode,
@@ -3460,7 +3471,7 @@ int ffa_align_plan_batch(const ffa_record* records, int64_t count, const ffa_ali
   // the edge arrays (8 bytes per frame and band boundary of the widest record)
   int64_t bands = 0, band_stride = 0, band_bytes = 0, band_lds = 0;
   const int64_t ws_band = ws;
-  if (!logits && K >= 8 && (!optimized || split)) {
+  if ((!logits && K >= 8 && (!optimized || split)) || band_tail) {
     int64_t nb_max = 1;
     for (int64_t i = 0; i < count; ++i) {
       const int64_t nb = (states_of(records[i]) + ffa::BAND_STATES - 1) / ffa::BAND_STATES;
@@ -3628,7 +3639,8 @@ int align_launch(const ffa_align_plan* plan, const ffa_align_options* o, const v
   const size_t lds = (size_t)in[I_LDS];
   const int64_t max_frames = in[I_MAX_FRAMES];
   const bool split = in[I_SPLIT] != 0;
-  p.tstate = split ? reinterpret_cast<ffa::TailState*>(ws + in[I_WS_TSTATE]) : nullptr;
+  p.tstate = (split || (optimized && in[I_BANDS] > 0)) ? reinterpret_cast<ffa::TailState*>(ws + in[I_WS_TSTATE])
+                                                       : nullptr;
   // the fused tail: optimized mode with greedy shortcuts, log-probabilities,
   // no split tail, at most 16 states per thread, and at most four chunks per
   // CU (larger grids run in several rounds of workgroups, and the hand-off's

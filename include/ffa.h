@@ -136,7 +136,8 @@ int ffa_align_describe(const ffa_align_plan* plan, const ffa_record* records,
  * and kept until the process ends.
  * A stream under graph capture that has none yet takes the two-launch form.
  * Batches of log-probabilities with a transcript of more than 1,024 states
- * (conventional mode, or optimized mode with a record of 2,048+ frames) run
+ * (conventional mode, or optimized mode with a record of 2,048+ frames; more
+ * than 4,096 states in optimized mode without repair rounds) run
  * the full DP in bands of 256 states, one workgroup each; the launch first
  * zeroes the bands' control words and edge arrays, which the plan places in
  * the workspace (no kernel of this entry writes memory it does not own). */

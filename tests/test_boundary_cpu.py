@@ -272,7 +272,8 @@ def test_logits_option_plans_statistics(lib):
 def test_banded_dp_plans_control_words_and_edge_arrays(lib):
     """Transcripts of more than 1,024 states run the banded DP (bands of 256
     states) in conventional mode and, under the split tail, for optimized
-    mode's early fallbacks; log-probability input only. The plan adds control
+    mode's fallbacks; without the split tail, transcripts of more than 4,096
+    states; log-probability input only. The plan adds control
     words (64 + B ints and two floats per record, 256-byte aligned) and 8 bytes
     per frame and band boundary of the widest record to the workspace."""
     wide = [(3000, 32, 2200, 0), (500, 32, 100, 0)]   # S = 4401 (18 bands) and 201 (1 band)
@@ -283,9 +284,19 @@ def test_banded_dp_plans_control_words_and_edge_arrays(lib):
     assert rc == 0 and rc2 == 0
     assert conv.workspace_bytes - conv_lg.workspace_bytes == band - stats
     rc, opt, _ = _plan(lib, wide)                     # T_max >= 2048: split tail, banded early fallbacks
-    rc2, opt_r0, _ = _plan(lib, wide, repair_rounds=0)  # no split tail, no banded DP
+    rc2, opt_lg, _ = _plan(lib, wide, logits=1)       # logits: one-workgroup DPs
     assert rc == 0 and rc2 == 0
-    assert opt.workspace_bytes - opt_r0.workspace_bytes == 256 + band  # + one 112-byte tail state per record
+    assert opt.workspace_bytes - opt_lg.workspace_bytes == band - stats
+    # no repair rounds (no split tail): K = 32 transcripts still hand their fallback to the
+    # banded DP, through one 112-byte tail state per record
+    rc, opt_r0, _ = _plan(lib, wide, repair_rounds=0)
+    rc2, opt_r0_lg, _ = _plan(lib, wide, repair_rounds=0, logits=1)
+    assert rc == 0 and rc2 == 0
+    assert opt_r0.workspace_bytes - opt_r0_lg.workspace_bytes == 256 + band - stats
+    k16 = [(3000, 32, 1500, 0), (500, 32, 100, 0)]   # S = 3001: K = 16, no banded DP without the split tail
+    rc, a, _ = _plan(lib, k16, repair_rounds=0)
+    rc2, b, _ = _plan(lib, k16, repair_rounds=0, logits=1)
+    assert rc == 0 and rc2 == 0 and b.workspace_bytes - a.workspace_bytes == stats
     narrow = [(3000, 32, 500, 0), (500, 32, 100, 0)]  # S = 1001: K = 4, one workgroup per record
     rc, conv, _ = _plan(lib, narrow, optimized=False)
     rc2, conv_lg, _ = _plan(lib, narrow, optimized=False, logits=1)

@@ -132,3 +132,47 @@ def test_repeated_calls_and_two_streams():
         assert_same({f: getattr(r, f).cpu().numpy() for f in FIELDS}, w1, where="stream 1 ")
     for r in out2:
         assert_same({f: getattr(r, f).cpu().numpy() for f in FIELDS}, w2, where="stream 2 ")
+
+
+def _op(es, ys, knobs):
+    import repair_cases as RC  # noqa: F401  (knob vectors)
+    e = [torch.from_numpy(np.ascontiguousarray(x)).cuda() for x in es]
+    y = [torch.from_numpy(np.ascontiguousarray(x, dtype=np.int64)).cuda() for x in ys]
+    k = knobs
+    with torch.inference_mode():
+        tensors, _ = torch.ops.fast_forced_aligner_cuda.align(
+            e, y, [0] * len(es), k["chunk_frames"], k["mode"], k["threads"], k["repair_rounds"],
+            k["optimization_pass"], k["variant"], k["repair_budget_frames"], k["repair_threads"],
+            k["compact_alphabet"], k["parallel_traceback"], k["overlap_fallback"], k["trace_min_frames"],
+            k["repair_min_frames"], k["frontier_reuse"], k["frontier_min_frames"], None, True)
+    return {f: t.cpu().numpy() for f, t in zip(FIELDS, tensors)}
+
+
+@pytest.mark.parametrize("knobs", [dict(repair_rounds=0), dict(overlap_fallback=False)],
+                         ids=["no_repair_rounds", "overlap_off"])
+def test_optimized_fallback_after_failed_seams(knobs):
+    """Optimized mode, transcripts of more than 4,096 states (K = 32) whose
+    seams still fail after the repair rounds: the fallback (cu:552-559) runs
+    as a banded DP after the tail, without the split tail (no repair rounds)
+    and with it (overlap fallback off)."""
+    import repair_cases as RC
+    rng = np.random.default_rng(552)
+    es, ys = [], []
+    for T, U in ((4600, 2200), (4300, 2100)):
+        e, y = _wide(rng, U, T)
+        # noisy spans: illegal seams around them; the 700-frame one makes any repair
+        # region exceed the 512-frame budget, so with overlap off no round repairs it
+        for start, width in ((900, 700), (2800, 150), (3700, 150)):
+            e[start:start + width] = workloads._log_softmax(2 * rng.standard_normal((width, 32)).astype(np.float32))
+        es.append(e)
+        ys.append(y)
+    e, y = _wide(rng, 150, 600)
+    es.append(e)
+    ys.append(y)
+    k = RC.knob_vector(**knobs)
+    print(f"band: optimized fallback after failed seams {knobs}", flush=True)
+    got = _op(es, ys, k)
+    want = O.align(es, ys, blank_id=[0] * len(es), options=RC.oracle_options(k), threads=8)
+    assert_same(got, want, where=f"fallback {knobs} ")
+    assert (got["stitched"][:2] == 0).all() and (got["status"][:2] == 0).all()  # the fallback aligned them
+
